@@ -1,0 +1,197 @@
+/*
+ * qwen3mi.h - C ABI of the MI355X (gfx950) kernels for the Qwen3 GRPO
+ * rollout-and-loss path.
+ *
+ * Every entry point:
+ *   - takes plain device pointers, element strides and sizes (no torch types);
+ *   - launches asynchronously on `stream` (a hipStream_t passed as void*;
+ *     NULL means the legacy default stream) and never synchronises, reads
+ *     device data on the host or allocates, so it can be captured into a
+ *     HIP graph;
+ *   - returns QMI_OK (0), a negative QMI_E* code when an argument is
+ *     rejected before launch (nothing is launched then), or a positive
+ *     hipError_t value when the launch itself failed.
+ *
+ * bf16 tensors are passed as raw 16-bit words.  Integer index tensors are
+ * int32 unless a parameter says int64.
+ */
+#ifndef QWEN3MI_H
+#define QWEN3MI_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QMI_OK 0
+#define QMI_E_NULL_POINTER (-1)
+#define QMI_E_BAD_SHAPE (-2)
+#define QMI_E_BAD_STRIDE (-3)
+#define QMI_E_UNSUPPORTED (-4)
+#define QMI_E_WORKSPACE_TOO_SMALL (-5)
+
+/* Human-readable text for a return code of any entry point. */
+const char* qmi_error_string(int code);
+
+/* Library version: major * 10000 + minor * 100 + patch. */
+int qmi_version(void);
+
+/*
+ * Slot-mapped KV store.
+ * Replaces `store_kvcache` / `_store_kvcache_kernel`
+ * (qwen3_naive.py:20-41), called from Qwen3Attention.forward_prefill
+ * (qwen3_naive.py:626) and forward_decode (qwen3_naive.py:668).
+ *
+ * For every token i < n_tokens with s = slot_mapping[i]:
+ *   k_cache[s*row_elems : (s+1)*row_elems] = key[i*key_row_stride : +row_elems]
+ *   v_cache[...same...]                    = value[i*value_row_stride : +row_elems]
+ * s == -1 skips the token, as in the reference.  Slots outside
+ * [0, n_slots) are also skipped instead of writing out of bounds.
+ * row_elems = kv_heads * head_dim (1024 for Qwen3-0.6B); n_slots =
+ * num_blocks * block_size.  Strides are in elements.
+ */
+int qmi_store_kvcache(const uint16_t* key, int64_t key_row_stride,
+                      const uint16_t* value, int64_t value_row_stride,
+                      uint16_t* k_cache, uint16_t* v_cache,
+                      const int32_t* slot_mapping, int64_t n_tokens,
+                      int64_t row_elems, int64_t n_slots, void* stream);
+
+/*
+ * Paged GQA decode attention (one query token per sequence).
+ * Replaces `flash_attn_with_kvcache(q.unsqueeze(1), k_cache, v_cache,
+ * cache_seqlens=context_lens + 1, block_table=block_tables,
+ * softmax_scale=scale, causal=True)` in Qwen3Attention.forward_decode
+ * (qwen3_naive.py:672-680).
+ *
+ * q      : [batch, num_q_heads, head_dim] bf16, element strides
+ *          q_seq_stride / q_head_stride, unit stride along head_dim.
+ * caches : [num_blocks, block_size, num_kv_heads, head_dim] bf16, contiguous.
+ * seqlens: int32 [batch]; sequence b attends to keys 0 .. seqlens[b] +
+ *          seqlen_bias - 1 (flash-attn's cache_seqlens = seqlens + bias;
+ *          forward_decode passes context_lens with bias 1).
+ * block_table: int32 [batch, bt_width] (row stride bt_stride), -1 padded.
+ * out    : [batch, num_q_heads, head_dim] bf16 with its own strides.
+ * workspace: fp32 scratch of at least qmi_paged_decode_workspace_bytes().
+ * q head h reads KV head h / (num_q_heads / num_kv_heads).
+ * Supported: head_dim 128, block_size 256, num_q_heads / num_kv_heads in
+ * {1, 2, 4, 8}.  pages_per_split <= 0 chooses the split size automatically.
+ * Pages whose table entry is outside [0, num_blocks) contribute nothing.
+ */
+int64_t qmi_paged_decode_workspace_bytes(int64_t batch, int64_t num_kv_heads,
+                                         int64_t num_q_heads, int64_t bt_width,
+                                         int64_t pages_per_split);
+
+int qmi_paged_decode_attention(const uint16_t* q, int64_t q_seq_stride, int64_t q_head_stride,
+                               const uint16_t* k_cache, const uint16_t* v_cache,
+                               int64_t num_blocks, int64_t block_size,
+                               int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                               const int32_t* seqlens, int32_t seqlen_bias,
+                               const int32_t* block_table, int64_t bt_stride, int64_t bt_width,
+                               int64_t batch, float scale,
+                               uint16_t* out, int64_t out_seq_stride, int64_t out_head_stride,
+                               float* workspace, int64_t workspace_bytes,
+                               int64_t pages_per_split, void* stream);
+
+/*
+ * Row-wise log-softmax gathered at one token per row.
+ * Replaces `F.log_softmax(logits.float(), -1).gather(-1, ids)` of
+ * forward_logprob (qwen3_grpo_train.py:46-53) and the rollout's
+ * `log_softmax(last_logits).gather(next_tokens)` (qwen3_naive.py:1649-1650).
+ *
+ * Rows are (b, t) for b < n_seq, t < n_tok; row (b, t) starts at
+ * logits + b*logit_seq_stride + t*logit_tok_stride and holds vocab bf16
+ * values with unit stride.  Its token is ids[b*id_seq_stride +
+ * t*id_tok_stride] (int64).  Outputs are fp32 [n_seq, n_tok] contiguous:
+ *   out_lp[b,t]  = logits[b,t,id] - logsumexp(logits[b,t,:])
+ *   out_lse[b,t] = logsumexp(logits[b,t,:])        (out_lse may be NULL)
+ * An id outside [0, vocab) yields NaN for that row.
+ */
+int qmi_logprob_gather(const uint16_t* logits, int64_t logit_seq_stride, int64_t logit_tok_stride,
+                       const int64_t* ids, int64_t id_seq_stride, int64_t id_tok_stride,
+                       int64_t n_seq, int64_t n_tok, int64_t vocab,
+                       float* out_lp, float* out_lse, void* stream);
+
+/*
+ * Group-normalised advantages.
+ * Replaces compute_grpo_advantage (qwen3_grpo_train.py:162-173):
+ *   A[i] = (r[i] - mean_g) / (std_g + eps)
+ * over the rows whose prompt_ids equal prompt_ids[i]; std is the unbiased
+ * (n-1) estimate, so a group of one row gives NaN as torch does.
+ * rewards fp32 [n], prompt_ids int64 [n], out fp32 [n].
+ */
+int qmi_grpo_advantage(const float* rewards, const int64_t* prompt_ids, int64_t n,
+                       float eps, float* out_adv, void* stream);
+
+#define QMI_REDUCE_TOKEN_MEAN 0   /* sum(l*m) / (sum(m) + 1e-8), qwen3_grpo_train.py:198 */
+#define QMI_REDUCE_SEQ_MEAN 1     /* mean_b( sum_t(l*m) / sum_t(m) ) */
+
+/*
+ * PPO clipped surrogate on given log-probabilities.
+ * Replaces ppo_clipped_loss (qwen3_grpo_train.py:184-199):
+ *   r = exp(new - old); l = -min(r*A, clamp(r, 1-clip, 1+clip)*A)
+ * new_lp / old_lp / mask: fp32 [n_seq, n_tok] contiguous.  adv is fp32
+ * addressed as adv[b*adv_seq_stride + t*adv_tok_stride]: strides (n_tok, 1)
+ * for the reference's per-token advantages (qwen3_grpo_train.py:269),
+ * (1, 0) for one advantage per sequence.
+ * Masked tokens (mask == 0) are skipped.  out_loss: fp32 scalar.
+ * out_dlp (may be NULL): fp32 [n_seq, n_tok], d loss / d new_lp, using
+ * torch's subgradients of min (ties split 1/2) and clamp (pass-through
+ * on the closed interval).
+ */
+int qmi_ppo_clipped_loss(const float* new_lp, const float* old_lp, const float* mask,
+                         const float* adv, int64_t adv_seq_stride, int64_t adv_tok_stride,
+                         int64_t n_seq, int64_t n_tok,
+                         float clip_eps, int32_t reduction,
+                         float* out_loss, float* out_dlp, void* stream);
+
+/*
+ * Fused GRPO loss step: log-softmax gather + group advantages + clipped
+ * masked loss, one streaming pass over the logits (the dominant cost).
+ * Combines qwen3_grpo_train.py:46-53 (forward_logprob's gather), :162-173
+ * (advantages), :269 (token expansion) and :184-199 (loss).
+ *
+ * Logit/id addressing as qmi_logprob_gather (pass shifted views for the
+ * logits[t-1] <-> ids[t] alignment).  old_lp, mask: fp32 [n_seq, n_tok]
+ * contiguous; rewards fp32 [n_seq]; prompt_ids int64 [n_seq].
+ * Outputs: out_lp, out_lse fp32 [n_seq, n_tok]; out_adv fp32 [n_seq];
+ * out_dlp fp32 [n_seq, n_tok] (d loss / d lp); out_loss fp32 scalar.
+ * workspace: qmi_grpo_fused_workspace_bytes(n_seq, n_tok) bytes, zeroed
+ * by the caller once before first use; the kernels leave it zeroed again.
+ */
+int64_t qmi_grpo_fused_workspace_bytes(int64_t n_seq, int64_t n_tok);
+
+int qmi_grpo_fused_loss(const uint16_t* logits, int64_t logit_seq_stride, int64_t logit_tok_stride,
+                        const int64_t* ids, int64_t id_seq_stride, int64_t id_tok_stride,
+                        int64_t n_seq, int64_t n_tok, int64_t vocab,
+                        const float* old_lp, const float* mask,
+                        const float* rewards, const int64_t* prompt_ids,
+                        float adv_eps, float clip_eps, int32_t reduction,
+                        float* out_lp, float* out_lse, float* out_adv, float* out_dlp,
+                        float* out_loss, void* workspace, int64_t workspace_bytes,
+                        void* stream);
+
+/*
+ * Backward of the log-softmax gather through the bf16 logits: for every
+ * row (b, t) and vocab entry v,
+ *   grad[b,t,v] = g * coef[b,t] * (1[v == id] - exp(logits[b,t,v] - lse[b,t]))
+ * rounded to bf16, where g = *grad_scale (a device fp32 scalar, e.g. the
+ * incoming gradient of the loss; NULL means 1).  Rows with coef == 0 are
+ * written as zeros without reading their logits.  This is the gradient
+ * that loss.backward() (qwen3_grpo_train.py:281) sends through
+ * log_softmax(logits.float()) back to the bf16 logits.
+ * grad is [n_seq, n_tok, vocab] bf16 with strides grad_seq_stride /
+ * grad_tok_stride; coef and lse are fp32 [n_seq, n_tok] contiguous.
+ */
+int qmi_logprob_gather_backward(const uint16_t* logits, int64_t logit_seq_stride, int64_t logit_tok_stride,
+                                const int64_t* ids, int64_t id_seq_stride, int64_t id_tok_stride,
+                                int64_t n_seq, int64_t n_tok, int64_t vocab,
+                                const float* lse, const float* coef, const float* grad_scale,
+                                uint16_t* grad, int64_t grad_seq_stride, int64_t grad_tok_stride,
+                                void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QWEN3MI_H */

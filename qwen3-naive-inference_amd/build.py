@@ -1,0 +1,98 @@
+"""Build the gfx950 shared library ``libqwen3mi.so`` from ``csrc/*.hip``.
+
+The library is a plain C-ABI ``.so`` (no torch types in any signature) built
+in-tree with ``hipcc`` so it travels with the source tree.  Each ``.hip``
+file is compiled to an object in parallel and then linked once.
+
+Usage: ``python -m`` is not possible for this package directory name, so run
+``python qwen3-naive-inference_amd/build.py`` or call :func:`build`.
+"""
+from __future__ import annotations
+
+import concurrent.futures
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+CSRC = PKG_DIR / "csrc"
+INCLUDE = PKG_DIR.parent / "include"
+LIB_NAME = "libqwen3mi.so"
+LIB_PATH = PKG_DIR / LIB_NAME
+OBJ_DIR = PKG_DIR / "_build"
+
+ARCH = "gfx950"
+
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-Wno-unused-function",
+    # Keep the compiler from emitting packed-fp32 VALU ops (v_pk_*_f32).
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    f"-I{INCLUDE}",
+]
+
+
+def hipcc_path() -> str:
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    cand = Path(rocm) / "bin" / "hipcc"
+    if cand.exists():
+        return str(cand)
+    found = shutil.which("hipcc")
+    if not found:
+        raise RuntimeError("hipcc not found: set ROCM_PATH or put hipcc on PATH")
+    return found
+
+
+def sources() -> list[Path]:
+    return sorted(CSRC.glob("*.hip"))
+
+
+def _compile(src: Path, verbose: bool) -> Path:
+    obj = OBJ_DIR / (src.stem + ".o")
+    cmd = [hipcc_path(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stdout}\n{res.stderr}")
+    # hipcc's host pass warns that it does not know the packed-fp32 feature.
+    noise = "is not a recognized feature for this target"
+    for line in (res.stdout + res.stderr).splitlines():
+        if line.strip() and noise not in line and verbose:
+            print(line)
+    return obj
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> Path:
+    """Compile every ``csrc/*.hip`` for gfx950 and link ``libqwen3mi.so``.
+
+    Always recompiles (this is the build check); returns the library path.
+    """
+    OBJ_DIR.mkdir(exist_ok=True)
+    srcs = sources()
+    if not srcs:
+        raise RuntimeError(f"no HIP sources under {CSRC}")
+    jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 4)), 16)
+    with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(lambda s: _compile(s, verbose), srcs))
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = [hipcc_path(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
+           *map(str, objs)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    path = build(verbose="-v" in sys.argv)
+    print(f"built {path}")

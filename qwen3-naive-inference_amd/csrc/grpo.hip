@@ -1,0 +1,547 @@
+// GRPO loss-step kernels: streaming log-softmax gather, group advantages,
+// PPO clipped masked loss, and the backward through the bf16 logits.
+//
+// Reference semantics (qwen3_grpo_train.py):
+//   forward_logprob         :46-53   lp[b,t] = log_softmax(float(logits[b,t]))[ids[b,t]]
+//   compute_grpo_advantage  :162-173 A = (r - mean_g) / (std_g + eps), unbiased std
+//   token advantages        :269     A_tok = A[:, None] * mask
+//   ppo_clipped_loss        :184-199 r = exp(new-old); l = -min(rA, clamp(r,1-e,1+e)A);
+//                                    L = sum(l*m) / (sum(m) + 1e-8)
+//
+// gfx950 design.  The logits read (n_rows x vocab bf16, 4.98 GB at the
+// 32x512x151936 loss step) is the whole cost, so one workgroup streams one
+// row with dwordx4 non-temporal loads, four chunks in flight per lane, and
+// keeps a per-lane (max, sum of exp2) pair rescaled once per 32 elements.
+// The pairs are merged with shuffles and one LDS exchange.  The fused
+// kernel finishes the loss in-kernel: each row writes its masked token
+// loss and d loss / d lp; the last row of every sequence (an atomic arrival
+// counter) sums that sequence and normalises its gradients; the last
+// sequence sums the sequences.  All sums run in a fixed order, so results
+// are deterministic, and the counters are reset by the finishers.
+#include "qmi_common.h"
+
+namespace {
+
+using namespace qmi;
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kUnroll = 4;
+
+// ---------------------------------------------------------------------------
+// Block-wide log-sum-exp of one row.  Returns lse2 = log2(sum(exp(x)))
+// (i.e. the natural lse times log2(e)) in every lane.
+template <bool VEC>
+__device__ __forceinline__ float row_lse2(const uint16_t* __restrict__ row, int64_t vocab,
+                                          float* sm_m, float* sm_s) {
+  const int tid = threadIdx.x;
+  float m2 = kNegBig, s = 0.f;
+  if (VEC) {
+    const int64_t nvec = vocab >> 3;
+    int64_t i = tid;
+    for (; i + (kUnroll - 1) * kThreads < nvec; i += kUnroll * kThreads) {
+      uint4 c[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) c[u] = load_u4_stream(row + ((i + u * kThreads) << 3));
+      float x[kUnroll * 8];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        x[u * 8 + 0] = bf16_lo(c[u].x); x[u * 8 + 1] = bf16_hi(c[u].x);
+        x[u * 8 + 2] = bf16_lo(c[u].y); x[u * 8 + 3] = bf16_hi(c[u].y);
+        x[u * 8 + 4] = bf16_lo(c[u].z); x[u * 8 + 5] = bf16_hi(c[u].z);
+        x[u * 8 + 6] = bf16_lo(c[u].w); x[u * 8 + 7] = bf16_hi(c[u].w);
+      }
+      float cm = x[0];
+#pragma unroll
+      for (int e = 1; e < kUnroll * 8; ++e) cm = fmaxf(cm, x[e]);
+      const float mn = fmaxf(m2, cm * kLog2e);
+      s *= fast_exp2(m2 - mn);
+      m2 = mn;
+#pragma unroll
+      for (int e = 0; e < kUnroll * 8; ++e) s += fast_exp2(fmaf(x[e], kLog2e, -mn));
+    }
+    for (; i < nvec; i += kThreads) {
+      const uint4 c = load_u4_stream(row + (i << 3));
+      float x[8];
+      x[0] = bf16_lo(c.x); x[1] = bf16_hi(c.x); x[2] = bf16_lo(c.y); x[3] = bf16_hi(c.y);
+      x[4] = bf16_lo(c.z); x[5] = bf16_hi(c.z); x[6] = bf16_lo(c.w); x[7] = bf16_hi(c.w);
+      float cm = x[0];
+#pragma unroll
+      for (int e = 1; e < 8; ++e) cm = fmaxf(cm, x[e]);
+      const float mn = fmaxf(m2, cm * kLog2e);
+      s *= fast_exp2(m2 - mn);
+      m2 = mn;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s += fast_exp2(fmaf(x[e], kLog2e, -mn));
+    }
+    for (int64_t j = (nvec << 3) + tid; j < vocab; j += kThreads) {
+      const float x = bf16_to_f32(row[j]) * kLog2e;
+      const float mn = fmaxf(m2, x);
+      s = s * fast_exp2(m2 - mn) + fast_exp2(x - mn);
+      m2 = mn;
+    }
+  } else {
+    for (int64_t j = tid; j < vocab; j += kThreads) {
+      const float x = bf16_to_f32(row[j]) * kLog2e;
+      const float mn = fmaxf(m2, x);
+      s = s * fast_exp2(m2 - mn) + fast_exp2(x - mn);
+      m2 = mn;
+    }
+  }
+  // Wave merge.
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const float mo = shfl_xor_f32(m2, off);
+    const float so = shfl_xor_f32(s, off);
+    lse2_merge(m2, s, mo, so);
+  }
+  const int wave = tid >> 6;
+  if ((tid & 63) == 0) {
+    sm_m[wave] = m2;
+    sm_s[wave] = s;
+  }
+  __syncthreads();
+  float M = sm_m[0], S = sm_s[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) lse2_merge(M, S, sm_m[w], sm_s[w]);
+  return M + log2f(S);
+}
+
+// Per-sequence group advantage (reference compute_grpo_advantage): scans the
+// prompt ids; one lane computes it.
+__device__ float group_advantage(const float* __restrict__ rewards,
+                                 const int64_t* __restrict__ prompt_ids, int64_t n, int64_t i,
+                                 float eps) {
+  const int64_t pid = prompt_ids[i];
+  float sum = 0.f;
+  int64_t cnt = 0;
+  for (int64_t j = 0; j < n; ++j)
+    if (prompt_ids[j] == pid) {
+      sum += rewards[j];
+      ++cnt;
+    }
+  const float mean = sum / (float)cnt;
+  float ss = 0.f;
+  for (int64_t j = 0; j < n; ++j)
+    if (prompt_ids[j] == pid) {
+      const float d = rewards[j] - mean;
+      ss += d * d;
+    }
+  // Unbiased estimate; cnt == 1 gives 0/0 = NaN exactly as torch.std().
+  const float stdv = sqrtf(ss / (float)(cnt - 1));
+  return (rewards[i] - mean) / (stdv + eps);
+}
+
+// Token term of the clipped surrogate and its derivative w.r.t. new_lp,
+// following torch's subgradients: min() splits ties 1/2-1/2 and clamp()
+// passes the gradient on the closed interval [lo, hi].
+__device__ __forceinline__ void ppo_token(float new_lp, float old_lp, float adv, float clip,
+                                          float* loss, float* dlp) {
+  const float r = expf(new_lp - old_lp);
+  const float lo = 1.0f - clip, hi = 1.0f + clip;
+  const float rc = fminf(fmaxf(r, lo), hi);
+  const float s1 = r * adv, s2 = rc * adv;
+  *loss = -fminf(s1, s2);
+  const float pass = (r >= lo && r <= hi) ? 1.f : 0.f;
+  float w;
+  if (s1 < s2) w = 1.f;
+  else if (s1 > s2) w = pass;
+  else w = 0.5f + 0.5f * pass;
+  *dlp = -adv * r * w;
+}
+
+// ---------------------------------------------------------------------------
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void logprob_rows(
+    const uint16_t* __restrict__ logits, int64_t lss, int64_t lts,
+    const int64_t* __restrict__ ids, int64_t iss, int64_t its, int64_t n_tok, int64_t vocab,
+    float* __restrict__ out_lp, float* __restrict__ out_lse) {
+  __shared__ float sm_m[kWaves], sm_s[kWaves];
+  const int64_t row = blockIdx.x;
+  const int64_t b = row / n_tok, t = row - b * n_tok;
+  const uint16_t* rp = logits + b * lss + t * lts;
+  const int64_t id = ids[b * iss + t * its];
+  const float lse2 = row_lse2<VEC>(rp, vocab, sm_m, sm_s);
+  if (threadIdx.x == 0) {
+    const float lse = lse2 * kLn2;
+    const float xid = (id >= 0 && id < vocab) ? bf16_to_f32(rp[id]) : __builtin_nanf("");
+    out_lp[row] = xid - lse;
+    if (out_lse) out_lse[row] = lse;
+  }
+}
+
+struct FusedWs {
+  uint32_t* seq_count;   // [n_seq]
+  uint32_t* all_count;   // [1]
+  float* seq_sum;        // [n_seq]  sum_t l*m
+  float* seq_msum;       // [n_seq]  sum_t m
+  float* tok_loss;       // [n_seq * n_tok]
+};
+
+__host__ __device__ inline int64_t align16(int64_t x) { return (x + 15) & ~(int64_t)15; }
+
+__host__ __device__ inline int64_t fused_ws_bytes(int64_t n_seq, int64_t n_tok) {
+  return align16(4 * n_seq) + align16(4) + 2 * align16(4 * n_seq) + align16(4 * n_seq * n_tok);
+}
+
+__device__ inline FusedWs fused_ws(void* base, int64_t n_seq, int64_t n_tok) {
+  char* p = reinterpret_cast<char*>(base);
+  FusedWs w;
+  w.seq_count = reinterpret_cast<uint32_t*>(p);
+  p += align16(4 * n_seq);
+  w.all_count = reinterpret_cast<uint32_t*>(p);
+  p += align16(4);
+  w.seq_sum = reinterpret_cast<float*>(p);
+  p += align16(4 * n_seq);
+  w.seq_msum = reinterpret_cast<float*>(p);
+  p += align16(4 * n_seq);
+  w.tok_loss = reinterpret_cast<float*>(p);
+  return w;
+}
+
+// Block-wide fixed-order sum (every lane gets the total).
+__device__ float block_sum(float x, float* sm) {
+  x = wave_sum(x);
+  const int wave = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sm[wave] = x;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) t += sm[w];
+  return t;
+}
+
+__device__ __forceinline__ uint32_t arrive(uint32_t* counter) {
+  return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void reset_counter(uint32_t* counter) {
+  __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void grpo_fused_rows(
+    const uint16_t* __restrict__ logits, int64_t lss, int64_t lts,
+    const int64_t* __restrict__ ids, int64_t iss, int64_t its, int64_t n_seq, int64_t n_tok,
+    int64_t vocab, const float* __restrict__ old_lp, const float* __restrict__ mask,
+    const float* __restrict__ rewards, const int64_t* __restrict__ prompt_ids, float adv_eps,
+    float clip, int reduction, float* __restrict__ out_lp, float* __restrict__ out_lse,
+    float* __restrict__ out_adv, float* __restrict__ out_dlp, float* __restrict__ out_loss,
+    void* __restrict__ ws_base) {
+  __shared__ float sm_m[kWaves], sm_s[kWaves], sm_red[kWaves];
+  __shared__ bool sm_last;
+  const FusedWs ws = fused_ws(ws_base, n_seq, n_tok);
+  const int64_t row = blockIdx.x;
+  const int64_t b = row / n_tok, t = row - b * n_tok;
+  const uint16_t* rp = logits + b * lss + t * lts;
+  const int64_t id = ids[b * iss + t * its];
+  const float lse2 = row_lse2<VEC>(rp, vocab, sm_m, sm_s);
+
+  if (threadIdx.x == 0) {
+    const float lse = lse2 * kLn2;
+    const float xid = (id >= 0 && id < vocab) ? bf16_to_f32(rp[id]) : __builtin_nanf("");
+    const float lp = xid - lse;
+    out_lp[row] = lp;
+    out_lse[row] = lse;
+    const float m = mask[row];
+    float tl = 0.f, tg = 0.f;
+    if (m != 0.f) {
+      const float adv = group_advantage(rewards, prompt_ids, n_seq, b, adv_eps);
+      float l, g;
+      ppo_token(lp, old_lp[row], adv, clip, &l, &g);
+      tl = l * m;
+      tg = g * m;
+    }
+    ws.tok_loss[row] = tl;
+    out_dlp[row] = tg;  // normalised by the sequence finisher below
+    __threadfence();
+    sm_last = (arrive(&ws.seq_count[b]) == (uint32_t)(n_tok - 1));
+  }
+  __syncthreads();
+  if (!sm_last) return;
+
+  // ---- last row of sequence b: per-sequence sums and gradient scaling ----
+  __threadfence();
+  float sl = 0.f, sm = 0.f;
+  for (int64_t j = threadIdx.x; j < n_tok; j += kThreads) {
+    sl += ws.tok_loss[b * n_tok + j];
+    sm += mask[b * n_tok + j];
+  }
+  sl = block_sum(sl, sm_red);
+  sm = block_sum(sm, sm_red);
+  float den;
+  if (reduction == QMI_REDUCE_TOKEN_MEAN) {
+    float all = 0.f;
+    for (int64_t j = threadIdx.x; j < n_seq * n_tok; j += kThreads) all += mask[j];
+    den = block_sum(all, sm_red) + 1e-8f;
+  } else {
+    den = (float)n_seq * (sm + 1e-8f);
+  }
+  const float inv = 1.0f / den;
+  for (int64_t j = threadIdx.x; j < n_tok; j += kThreads) out_dlp[b * n_tok + j] *= inv;
+  if (threadIdx.x == 0) {
+    ws.seq_sum[b] = sl;
+    ws.seq_msum[b] = sm;
+    out_adv[b] = group_advantage(rewards, prompt_ids, n_seq, b, adv_eps);
+    reset_counter(&ws.seq_count[b]);
+    __threadfence();
+    sm_last = (arrive(ws.all_count) == (uint32_t)(n_seq - 1));
+  }
+  __syncthreads();
+  if (!sm_last) return;
+
+  // ---- last sequence: the scalar loss in sequence order ----
+  __threadfence();
+  if (threadIdx.x == 0) {
+    float loss;
+    if (reduction == QMI_REDUCE_TOKEN_MEAN) {
+      float num = 0.f, msum = 0.f;
+      for (int64_t j = 0; j < n_seq; ++j) {
+        num += ws.seq_sum[j];
+        msum += ws.seq_msum[j];
+      }
+      loss = num / (msum + 1e-8f);
+    } else {
+      float acc = 0.f;
+      for (int64_t j = 0; j < n_seq; ++j) acc += ws.seq_sum[j] / (ws.seq_msum[j] + 1e-8f);
+      loss = acc / (float)n_seq;
+    }
+    *out_loss = loss;
+    reset_counter(ws.all_count);
+  }
+}
+
+// ---------------------------------------------------------------------------
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void logprob_backward_rows(
+    const uint16_t* __restrict__ logits, int64_t lss, int64_t lts,
+    const int64_t* __restrict__ ids, int64_t iss, int64_t its, int64_t n_tok, int64_t vocab,
+    const float* __restrict__ lse, const float* __restrict__ coef,
+    const float* __restrict__ grad_scale, uint16_t* __restrict__ grad, int64_t gss, int64_t gts) {
+  const int64_t row = blockIdx.x;
+  const int64_t b = row / n_tok, t = row - b * n_tok;
+  const uint16_t* rp = logits + b * lss + t * lts;
+  uint16_t* gp = grad + b * gss + t * gts;
+  const float c = coef[row] * (grad_scale ? *grad_scale : 1.0f);
+  const int64_t id = ids[b * iss + t * its];
+  const int tid = threadIdx.x;
+  if (c == 0.f) {
+    if (VEC) {
+      const int64_t nvec = vocab >> 3;
+      for (int64_t i = tid; i < nvec; i += kThreads)
+        reinterpret_cast<uint4*>(gp)[i] = make_uint4(0, 0, 0, 0);
+      for (int64_t j = (nvec << 3) + tid; j < vocab; j += kThreads) gp[j] = 0;
+    } else {
+      for (int64_t j = tid; j < vocab; j += kThreads) gp[j] = 0;
+    }
+    return;
+  }
+  const float l2 = lse[row] * kLog2e;
+  if (VEC) {
+    const int64_t nvec = vocab >> 3;
+    for (int64_t i = tid; i < nvec; i += kThreads) {
+      const uint4 x = load_u4_stream(rp + (i << 3));
+      const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+      uint32_t o[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int64_t v0 = (i << 3) + 2 * k;
+        float g0 = -c * fast_exp2(fmaf(bf16_lo(w[k]), kLog2e, -l2));
+        float g1 = -c * fast_exp2(fmaf(bf16_hi(w[k]), kLog2e, -l2));
+        if (v0 == id) g0 += c;
+        if (v0 + 1 == id) g1 += c;
+        o[k] = pack_bf16x2(g0, g1);
+      }
+      reinterpret_cast<uint4*>(gp)[i] = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+    for (int64_t j = (nvec << 3) + tid; j < vocab; j += kThreads) {
+      float g = -c * fast_exp2(fmaf(bf16_to_f32(rp[j]), kLog2e, -l2));
+      if (j == id) g += c;
+      gp[j] = f32_to_bf16(g);
+    }
+  } else {
+    for (int64_t j = tid; j < vocab; j += kThreads) {
+      float g = -c * fast_exp2(fmaf(bf16_to_f32(rp[j]), kLog2e, -l2));
+      if (j == id) g += c;
+      gp[j] = f32_to_bf16(g);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void advantage_kernel(const float* __restrict__ rewards,
+                                                             const int64_t* __restrict__ pids,
+                                                             int64_t n, float eps,
+                                                             float* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i < n) out[i] = group_advantage(rewards, pids, n, i, eps);
+}
+
+// Single workgroup, fixed summation order (deterministic).
+constexpr int kLossThreads = 1024;
+__global__ __launch_bounds__(kLossThreads) void ppo_loss_kernel(
+    const float* __restrict__ new_lp, const float* __restrict__ old_lp,
+    const float* __restrict__ mask, const float* __restrict__ adv, int64_t ass, int64_t ats,
+    int64_t n_seq, int64_t n_tok, float clip, int reduction, float* __restrict__ out_loss,
+    float* __restrict__ out_dlp) {
+  __shared__ float sm[kLossThreads / 64];
+  const int tid = threadIdx.x;
+  auto bsum = [&](float x) {
+    x = wave_sum(x);
+    __syncthreads();
+    if ((tid & 63) == 0) sm[tid >> 6] = x;
+    __syncthreads();
+    float t = 0.f;
+    for (int w = 0; w < kLossThreads / 64; ++w) t += sm[w];
+    return t;
+  };
+  float all_m = 0.f;
+  for (int64_t j = tid; j < n_seq * n_tok; j += kLossThreads) all_m += mask[j];
+  all_m = bsum(all_m);
+  float num = 0.f, acc = 0.f;
+  for (int64_t b = 0; b < n_seq; ++b) {
+    float sl = 0.f, smk = 0.f;
+    for (int64_t t = tid; t < n_tok; t += kLossThreads) {
+      const int64_t k = b * n_tok + t;
+      const float m = mask[k];
+      smk += m;
+      if (m != 0.f) {
+        float l, g;
+        ppo_token(new_lp[k], old_lp[k], adv[b * ass + t * ats], clip, &l, &g);
+        sl += l * m;
+      }
+    }
+    sl = bsum(sl);
+    smk = bsum(smk);
+    num += sl;
+    acc += sl / (smk + 1e-8f);
+    if (out_dlp) {
+      const float inv = reduction == QMI_REDUCE_TOKEN_MEAN ? 1.0f / (all_m + 1e-8f)
+                                                           : 1.0f / ((float)n_seq * (smk + 1e-8f));
+      for (int64_t t = tid; t < n_tok; t += kLossThreads) {
+        const int64_t k = b * n_tok + t;
+        const float m = mask[k];
+        float g = 0.f;
+        if (m != 0.f) {
+          float l;
+          ppo_token(new_lp[k], old_lp[k], adv[b * ass + t * ats], clip, &l, &g);
+          g *= m * inv;
+        }
+        out_dlp[k] = g;
+      }
+    }
+  }
+  if (tid == 0)
+    *out_loss = reduction == QMI_REDUCE_TOKEN_MEAN ? num / (all_m + 1e-8f) : acc / (float)n_seq;
+}
+
+inline bool rows_vec_ok(const uint16_t* p, int64_t s1, int64_t s2) {
+  return ((reinterpret_cast<uintptr_t>(p) & 15u) == 0) && (s1 % 8 == 0) && (s2 % 8 == 0);
+}
+
+}  // namespace
+
+extern "C" int qmi_logprob_gather(const uint16_t* logits, int64_t lss, int64_t lts,
+                                  const int64_t* ids, int64_t iss, int64_t its, int64_t n_seq,
+                                  int64_t n_tok, int64_t vocab, float* out_lp, float* out_lse,
+                                  void* stream) {
+  if (n_seq < 0 || n_tok < 0 || vocab <= 0) return QMI_E_BAD_SHAPE;
+  if (n_seq * n_tok == 0) return QMI_OK;
+  if (!logits || !ids || !out_lp) return QMI_E_NULL_POINTER;
+  if (n_seq * n_tok > 0x7fffffffLL) return QMI_E_UNSUPPORTED;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)(n_seq * n_tok));
+  if (rows_vec_ok(logits, lss, lts))
+    hipLaunchKernelGGL(logprob_rows<true>, grid, dim3(kThreads), 0, s, logits, lss, lts, ids, iss,
+                       its, n_tok, vocab, out_lp, out_lse);
+  else
+    hipLaunchKernelGGL(logprob_rows<false>, grid, dim3(kThreads), 0, s, logits, lss, lts, ids,
+                       iss, its, n_tok, vocab, out_lp, out_lse);
+  QMI_RETURN_LAUNCH_STATUS();
+}
+
+extern "C" int qmi_grpo_advantage(const float* rewards, const int64_t* prompt_ids, int64_t n,
+                                  float eps, float* out_adv, void* stream) {
+  if (n < 0) return QMI_E_BAD_SHAPE;
+  if (n == 0) return QMI_OK;
+  if (!rewards || !prompt_ids || !out_adv) return QMI_E_NULL_POINTER;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(advantage_kernel, dim3((unsigned)((n + kThreads - 1) / kThreads)),
+                     dim3(kThreads), 0, s, rewards, prompt_ids, n, eps, out_adv);
+  QMI_RETURN_LAUNCH_STATUS();
+}
+
+extern "C" int qmi_ppo_clipped_loss(const float* new_lp, const float* old_lp, const float* mask,
+                                    const float* adv, int64_t adv_seq_stride,
+                                    int64_t adv_tok_stride, int64_t n_seq, int64_t n_tok,
+                                    float clip_eps, int32_t reduction, float* out_loss,
+                                    float* out_dlp, void* stream) {
+  if (n_seq <= 0 || n_tok < 0) return QMI_E_BAD_SHAPE;
+  if (!new_lp || !old_lp || !mask || !adv || !out_loss) return QMI_E_NULL_POINTER;
+  if (reduction != QMI_REDUCE_TOKEN_MEAN && reduction != QMI_REDUCE_SEQ_MEAN)
+    return QMI_E_UNSUPPORTED;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(ppo_loss_kernel, dim3(1), dim3(kLossThreads), 0, s, new_lp, old_lp, mask,
+                     adv, adv_seq_stride, adv_tok_stride, n_seq, n_tok, clip_eps, (int)reduction,
+                     out_loss, out_dlp);
+  QMI_RETURN_LAUNCH_STATUS();
+}
+
+extern "C" int64_t qmi_grpo_fused_workspace_bytes(int64_t n_seq, int64_t n_tok) {
+  if (n_seq <= 0 || n_tok <= 0) return 0;
+  return fused_ws_bytes(n_seq, n_tok);
+}
+
+extern "C" int qmi_grpo_fused_loss(const uint16_t* logits, int64_t lss, int64_t lts,
+                                   const int64_t* ids, int64_t iss, int64_t its, int64_t n_seq,
+                                   int64_t n_tok, int64_t vocab, const float* old_lp,
+                                   const float* mask, const float* rewards,
+                                   const int64_t* prompt_ids, float adv_eps, float clip_eps,
+                                   int32_t reduction, float* out_lp, float* out_lse,
+                                   float* out_adv, float* out_dlp, float* out_loss,
+                                   void* workspace, int64_t workspace_bytes, void* stream) {
+  if (n_seq <= 0 || n_tok <= 0 || vocab <= 0) return QMI_E_BAD_SHAPE;
+  if (!logits || !ids || !old_lp || !mask || !rewards || !prompt_ids || !out_lp || !out_lse ||
+      !out_adv || !out_dlp || !out_loss || !workspace)
+    return QMI_E_NULL_POINTER;
+  if (reduction != QMI_REDUCE_TOKEN_MEAN && reduction != QMI_REDUCE_SEQ_MEAN)
+    return QMI_E_UNSUPPORTED;
+  if (n_seq * n_tok > 0x7fffffffLL) return QMI_E_UNSUPPORTED;
+  if (workspace_bytes < fused_ws_bytes(n_seq, n_tok)) return QMI_E_WORKSPACE_TOO_SMALL;
+  if (reinterpret_cast<uintptr_t>(workspace) & 15u) return QMI_E_BAD_STRIDE;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)(n_seq * n_tok));
+  if (rows_vec_ok(logits, lss, lts))
+    hipLaunchKernelGGL(grpo_fused_rows<true>, grid, dim3(kThreads), 0, s, logits, lss, lts, ids,
+                       iss, its, n_seq, n_tok, vocab, old_lp, mask, rewards, prompt_ids, adv_eps,
+                       clip_eps, (int)reduction, out_lp, out_lse, out_adv, out_dlp, out_loss,
+                       workspace);
+  else
+    hipLaunchKernelGGL(grpo_fused_rows<false>, grid, dim3(kThreads), 0, s, logits, lss, lts, ids,
+                       iss, its, n_seq, n_tok, vocab, old_lp, mask, rewards, prompt_ids, adv_eps,
+                       clip_eps, (int)reduction, out_lp, out_lse, out_adv, out_dlp, out_loss,
+                       workspace);
+  QMI_RETURN_LAUNCH_STATUS();
+}
+
+extern "C" int qmi_logprob_gather_backward(const uint16_t* logits, int64_t lss, int64_t lts,
+                                           const int64_t* ids, int64_t iss, int64_t its,
+                                           int64_t n_seq, int64_t n_tok, int64_t vocab,
+                                           const float* lse, const float* coef,
+                                           const float* grad_scale, uint16_t* grad, int64_t gss,
+                                           int64_t gts, void* stream) {
+  if (n_seq < 0 || n_tok < 0 || vocab <= 0) return QMI_E_BAD_SHAPE;
+  if (n_seq * n_tok == 0) return QMI_OK;
+  if (!logits || !ids || !lse || !coef || !grad) return QMI_E_NULL_POINTER;
+  if (n_seq * n_tok > 0x7fffffffLL) return QMI_E_UNSUPPORTED;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)(n_seq * n_tok));
+  if (rows_vec_ok(logits, lss, lts) && rows_vec_ok(grad, gss, gts))
+    hipLaunchKernelGGL(logprob_backward_rows<true>, grid, dim3(kThreads), 0, s, logits, lss, lts,
+                       ids, iss, its, n_tok, vocab, lse, coef, grad_scale, grad, gss, gts);
+  else
+    hipLaunchKernelGGL(logprob_backward_rows<false>, grid, dim3(kThreads), 0, s, logits, lss,
+                       lts, ids, iss, its, n_tok, vocab, lse, coef, grad_scale, grad, gss, gts);
+  QMI_RETURN_LAUNCH_STATUS();
+}

@@ -1,0 +1,321 @@
+"""Python shims over the C ABI: validate, then launch on torch's current stream.
+
+Each shim keeps the argument names, order and meaning of the reference call it
+replaces.  Validation failures raise ``ValueError`` before anything is
+launched; a failed launch raises ``QmiError``.  All outputs and workspaces are
+allocated through torch's caching allocator (graph-capture safe); the kernels
+never allocate, synchronise or read device data on the host.
+"""
+from __future__ import annotations
+
+import torch
+
+from ._lib import check, lib, stream_handle
+
+BLOCK_SIZE = 256
+HEAD_DIM = 128
+
+REDUCTIONS = {"token": 0, "token_mean": 0, "seq": 1, "seq_mean": 1}
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _require_cuda(name: str, t: torch.Tensor) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise ValueError(f"{name} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be a GPU tensor (got {t.device})")
+
+
+def _require_dtype(name: str, t: torch.Tensor, *dtypes: torch.dtype) -> None:
+    if t.dtype not in dtypes:
+        raise ValueError(f"{name} must have dtype in {dtypes}, got {t.dtype}")
+
+
+def _as_i32(name: str, t: torch.Tensor) -> torch.Tensor:
+    _require_cuda(name, t)
+    if t.dtype == torch.int32:
+        return t
+    if t.dtype in (torch.int64, torch.int16, torch.uint8, torch.int8):
+        return t.to(torch.int32)
+    raise ValueError(f"{name} must be an integer tensor, got {t.dtype}")
+
+
+# ---------------------------------------------------------------------------
+# KV store (qwen3_naive.py:20-41)
+# ---------------------------------------------------------------------------
+def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
+                  v_cache: torch.Tensor, slot_mapping: torch.Tensor) -> None:
+    """Write ``key[i]`` / ``value[i]`` into cache row ``slot_mapping[i]`` (-1 skips).
+
+    ``key``/``value``: ``[N, kv_heads, head_dim]`` bf16 whose inner
+    ``[kv_heads, head_dim]`` block is contiguous (``value`` may be a strided
+    view of the fused qkv projection).  ``k_cache``/``v_cache``: contiguous
+    paged pools ``[num_blocks, block_size, kv_heads, head_dim]``.
+    """
+    for n, t in (("key", key), ("value", value), ("k_cache", k_cache), ("v_cache", v_cache)):
+        _require_cuda(n, t)
+        _require_dtype(n, t, torch.bfloat16)
+    if key.dim() != 3 or value.shape != key.shape:
+        raise ValueError(f"key/value must be [N, H, D] of equal shape, got {tuple(key.shape)} "
+                         f"and {tuple(value.shape)}")
+    n_tok, h, d = key.shape
+    row = h * d
+    for n, t in (("key", key), ("value", value)):
+        if t.stride(2) != 1 or t.stride(1) != d:
+            raise ValueError(f"{n}'s [heads, head_dim] block must be contiguous")
+    for n, t in (("k_cache", k_cache), ("v_cache", v_cache)):
+        if not t.is_contiguous() or t.numel() % row != 0:
+            raise ValueError(f"{n} must be contiguous with rows of {row} elements")
+    if k_cache.shape != v_cache.shape:
+        raise ValueError("k_cache and v_cache must have the same shape")
+    slots = _as_i32("slot_mapping", slot_mapping)
+    if slots.dim() != 1 or slots.shape[0] != n_tok:
+        raise ValueError(f"slot_mapping must be [{n_tok}], got {tuple(slots.shape)}")
+    if not slots.is_contiguous():
+        slots = slots.contiguous()
+    if n_tok == 0:
+        return
+    st = lib().qmi_store_kvcache(key.data_ptr(), key.stride(0), value.data_ptr(), value.stride(0),
+                                 k_cache.data_ptr(), v_cache.data_ptr(), slots.data_ptr(), n_tok,
+                                 row, k_cache.numel() // row, stream_handle(key.device))
+    check(st, "store_kvcache")
+
+
+# ---------------------------------------------------------------------------
+# Paged decode attention (flash_attn_with_kvcache at qwen3_naive.py:672-680)
+# ---------------------------------------------------------------------------
+def paged_decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                           cache_seqlens: torch.Tensor, block_table: torch.Tensor,
+                           softmax_scale: float, seqlen_bias: int = 0,
+                           out: torch.Tensor | None = None,
+                           pages_per_split: int = 0) -> torch.Tensor:
+    """GQA attention of one query per sequence over its paged KV.
+
+    ``q``: ``[B, Hq, D]`` bf16 (unit stride along D).  Sequence ``b`` attends
+    to keys ``0 .. cache_seqlens[b] + seqlen_bias - 1`` (flash-attn's
+    ``cache_seqlens``; ``forward_decode`` passes ``context_lens`` with bias 1).
+    Returns ``out`` ``[B, Hq, D]`` bf16.
+    """
+    for n, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache)):
+        _require_cuda(n, t)
+        _require_dtype(n, t, torch.bfloat16)
+    if q.dim() != 3:
+        raise ValueError(f"q must be [B, Hq, D], got {tuple(q.shape)}")
+    bsz, hq, d = q.shape
+    if k_cache.dim() != 4 or k_cache.shape != v_cache.shape:
+        raise ValueError("caches must be [num_blocks, block_size, Hkv, D] of equal shape")
+    nb, bs, hkv, dk = k_cache.shape
+    if d != HEAD_DIM or dk != HEAD_DIM or bs != BLOCK_SIZE:
+        raise ValueError(f"supported: head_dim {HEAD_DIM}, block_size {BLOCK_SIZE}; got "
+                         f"q D={d}, cache {tuple(k_cache.shape)}")
+    if hq % hkv != 0 or (hq // hkv) not in (1, 2, 4, 8):
+        raise ValueError(f"GQA ratio Hq/Hkv must be 1, 2, 4 or 8 (Hq={hq}, Hkv={hkv})")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("caches must be contiguous")
+    if q.stride(2) != 1 or q.stride(0) % 8 or q.stride(1) % 8:
+        q = q.contiguous()
+    seqlens = _as_i32("cache_seqlens", cache_seqlens)
+    bt = _as_i32("block_table", block_table)
+    if seqlens.dim() != 1 or seqlens.shape[0] != bsz:
+        raise ValueError(f"cache_seqlens must be [{bsz}]")
+    if not seqlens.is_contiguous():
+        seqlens = seqlens.contiguous()
+    if bt.dim() != 2 or bt.shape[0] != bsz or bt.shape[1] < 1:
+        raise ValueError(f"block_table must be [{bsz}, W>=1], got {tuple(bt.shape)}")
+    if bt.stride(1) != 1:
+        bt = bt.contiguous()
+    if out is None:
+        out = torch.empty((bsz, hq, d), dtype=torch.bfloat16, device=q.device)
+    else:
+        _require_cuda("out", out)
+        _require_dtype("out", out, torch.bfloat16)
+        if out.shape != (bsz, hq, d) or out.stride(2) != 1:
+            raise ValueError("out must be [B, Hq, D] with unit stride along D")
+    if bsz == 0:
+        return out
+    L = lib()
+    wbytes = L.qmi_paged_decode_workspace_bytes(bsz, hkv, hq, bt.shape[1], pages_per_split)
+    ws = torch.empty((max(wbytes, 4) // 4,), dtype=torch.float32, device=q.device)
+    st = L.qmi_paged_decode_attention(
+        q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(), nb, bs,
+        hq, hkv, d, seqlens.data_ptr(), int(seqlen_bias), bt.data_ptr(), bt.stride(0),
+        bt.shape[1], bsz, float(softmax_scale), out.data_ptr(), out.stride(0), out.stride(1),
+        ws.data_ptr(), ws.numel() * 4, int(pages_per_split), stream_handle(q.device))
+    check(st, "paged_decode_attention")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Log-softmax gather (qwen3_grpo_train.py:46-53)
+# ---------------------------------------------------------------------------
+def _rows_view(logits: torch.Tensor, ids: torch.Tensor):
+    """Normalise ``logits`` to [B, T, V] and ``ids`` to [B, T] views."""
+    _require_cuda("logits", logits)
+    _require_dtype("logits", logits, torch.bfloat16)
+    _require_cuda("ids", ids)
+    _require_dtype("ids", ids, torch.int64)
+    if logits.dim() == 2:
+        logits = logits.unsqueeze(0)
+    if ids.dim() == 1:
+        ids = ids.unsqueeze(0)
+    if logits.dim() != 3 or ids.dim() != 2 or tuple(logits.shape[:2]) != tuple(ids.shape):
+        raise ValueError(f"logits [B,T,V] / ids [B,T] mismatch: {tuple(logits.shape)} vs "
+                         f"{tuple(ids.shape)}")
+    if logits.stride(2) != 1:
+        logits = logits.contiguous()
+    return logits, ids
+
+
+def logprob_gather(logits: torch.Tensor, ids: torch.Tensor, need_lse: bool = True):
+    """``log_softmax(logits.float(), -1).gather(-1, ids[..., None])[..., 0]`` and the row lse.
+
+    ``logits``: ``[B, T, V]`` (or ``[N, V]``) bf16 with unit vocab stride;
+    ``ids``: int64 ``[B, T]`` (or ``[N]``).  Returns fp32 ``(lp, lse)`` shaped
+    like ``ids``.
+    """
+    shape = ids.shape
+    lg, ii = _rows_view(logits, ids)
+    bsz, t, v = lg.shape
+    lp = torch.empty((bsz, t), dtype=torch.float32, device=lg.device)
+    lse = torch.empty((bsz, t), dtype=torch.float32, device=lg.device) if need_lse else None
+    st = lib().qmi_logprob_gather(lg.data_ptr(), lg.stride(0), lg.stride(1), ii.data_ptr(),
+                                  ii.stride(0), ii.stride(1), bsz, t, v, lp.data_ptr(),
+                                  _ptr(lse), stream_handle(lg.device))
+    check(st, "logprob_gather")
+    return lp.view(shape), (lse.view(shape) if lse is not None else None)
+
+
+def logprob_gather_backward(logits: torch.Tensor, ids: torch.Tensor, lse: torch.Tensor,
+                            coef: torch.Tensor, grad_scale: torch.Tensor | None = None,
+                            out: torch.Tensor | None = None) -> torch.Tensor:
+    """``grad[b,t,v] = g * coef[b,t] * (1[v==id] - exp(logits[b,t,v] - lse[b,t]))`` in bf16."""
+    lshape = logits.shape
+    lg, ii = _rows_view(logits, ids)
+    bsz, t, v = lg.shape
+    coef = coef.reshape(bsz, t).float().contiguous()
+    lse = lse.reshape(bsz, t).float().contiguous()
+    if grad_scale is not None:
+        grad_scale = grad_scale.reshape(1).float().contiguous()
+    if out is None:
+        out = torch.empty((bsz, t, v), dtype=torch.bfloat16, device=lg.device)
+    else:
+        out = out.view(bsz, t, v)
+        if out.stride(2) != 1:
+            raise ValueError("grad out must have unit vocab stride")
+    st = lib().qmi_logprob_gather_backward(
+        lg.data_ptr(), lg.stride(0), lg.stride(1), ii.data_ptr(), ii.stride(0), ii.stride(1),
+        bsz, t, v, lse.data_ptr(), coef.data_ptr(), _ptr(grad_scale), out.data_ptr(),
+        out.stride(0), out.stride(1), stream_handle(lg.device))
+    check(st, "logprob_gather_backward")
+    return out.view(lshape)
+
+
+# ---------------------------------------------------------------------------
+# Advantages / clipped loss (qwen3_grpo_train.py:162-199)
+# ---------------------------------------------------------------------------
+def grpo_advantage(rewards: torch.Tensor, prompt_ids: torch.Tensor, eps: float = 1e-8):
+    """Group-normalised advantages ``(r - mean_g) / (std_g + eps)`` (unbiased std)."""
+    _require_cuda("rewards", rewards)
+    _require_cuda("prompt_ids", prompt_ids)
+    r = rewards.reshape(-1).float().contiguous()
+    p = prompt_ids.reshape(-1).to(torch.int64).contiguous()
+    if r.shape != p.shape:
+        raise ValueError("rewards and prompt_ids must have the same length")
+    out = torch.empty_like(r)
+    if r.numel():
+        check(lib().qmi_grpo_advantage(r.data_ptr(), p.data_ptr(), r.numel(), float(eps),
+                                       out.data_ptr(), stream_handle(r.device)),
+              "grpo_advantage")
+    return out
+
+
+def ppo_clipped_loss_fwd(new_lp: torch.Tensor, old_lp: torch.Tensor, adv: torch.Tensor,
+                         mask: torch.Tensor, clip_eps: float = 0.2, reduction: str = "token",
+                         need_grad: bool = True):
+    """Clipped surrogate on ``[B, T]`` log-probs; ``adv`` is ``[B, T]`` or ``[B]``.
+
+    Returns ``(loss, dloss_dnew)`` (fp32 scalar tensor, fp32 ``[B, T]`` or None).
+    """
+    for n, t in (("new_lp", new_lp), ("old_lp", old_lp), ("mask", mask), ("adv", adv)):
+        _require_cuda(n, t)
+    if new_lp.dim() == 1:
+        new_lp, old_lp, mask = new_lp[None], old_lp[None], mask[None]
+        adv = adv[None] if adv.dim() == 1 and adv.shape[0] == new_lp.shape[1] else adv
+    bsz, t = new_lp.shape
+    nw = new_lp.float().contiguous()
+    od = old_lp.float().reshape(bsz, t).contiguous()
+    mk = mask.float().reshape(bsz, t).contiguous()
+    av = adv.float()
+    if av.dim() == 1 and av.shape[0] == bsz:
+        av = av.contiguous()
+        ass, ats = 1, 0
+    else:
+        av = av.reshape(bsz, t).contiguous()
+        ass, ats = t, 1
+    loss = torch.empty((), dtype=torch.float32, device=nw.device)
+    dlp = torch.empty((bsz, t), dtype=torch.float32, device=nw.device) if need_grad else None
+    check(lib().qmi_ppo_clipped_loss(nw.data_ptr(), od.data_ptr(), mk.data_ptr(), av.data_ptr(),
+                                     ass, ats, bsz, t, float(clip_eps), REDUCTIONS[reduction],
+                                     loss.data_ptr(), _ptr(dlp), stream_handle(nw.device)),
+          "ppo_clipped_loss")
+    return loss, dlp
+
+
+_FUSED_WS: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def _fused_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Cached zero-initialised workspace per (device, stream).
+
+    The fused kernel leaves its arrival counters at zero when it finishes, so
+    the buffer is zeroed only when it is (re)allocated.  Calls on the same
+    stream are ordered; calls on different streams get different buffers.
+    """
+    key = (device.index if device.index is not None else torch.cuda.current_device(),
+           stream_handle(device))
+    ws = _FUSED_WS.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(((nbytes + 15) // 16) * 16, dtype=torch.uint8, device=device)
+        _FUSED_WS[key] = ws
+    return ws
+
+
+def grpo_fused_forward(logits: torch.Tensor, ids: torch.Tensor, old_lp: torch.Tensor,
+                       mask: torch.Tensor, rewards: torch.Tensor, prompt_ids: torch.Tensor,
+                       adv_eps: float = 1e-8, clip_eps: float = 0.2, reduction: str = "token"):
+    """One streaming pass: per-token logprob + lse, group advantages, loss, d loss / d lp.
+
+    ``logits [B, T, V]`` bf16 rows are aligned with ``ids [B, T]`` (pass
+    ``logits[:, :-1]`` / ``ids[:, 1:]`` for next-token alignment).
+    Returns a dict of fp32 tensors: loss (scalar), lp, lse, dlp ``[B, T]``, adv ``[B]``.
+    """
+    lg, ii = _rows_view(logits, ids)
+    bsz, t, v = lg.shape
+    dev = lg.device
+    od = old_lp.float().reshape(bsz, t).contiguous()
+    mk = mask.float().reshape(bsz, t).contiguous()
+    rw = rewards.float().reshape(bsz).contiguous()
+    pid = prompt_ids.to(torch.int64).reshape(bsz).contiguous()
+    lp = torch.empty((bsz, t), dtype=torch.float32, device=dev)
+    lse = torch.empty_like(lp)
+    dlp = torch.empty_like(lp)
+    adv = torch.empty((bsz,), dtype=torch.float32, device=dev)
+    loss = torch.empty((), dtype=torch.float32, device=dev)
+    L = lib()
+    nbytes = L.qmi_grpo_fused_workspace_bytes(bsz, t)
+    ws = _fused_workspace(dev, nbytes)
+    check(L.qmi_grpo_fused_loss(lg.data_ptr(), lg.stride(0), lg.stride(1), ii.data_ptr(),
+                                ii.stride(0), ii.stride(1), bsz, t, v, od.data_ptr(),
+                                mk.data_ptr(), rw.data_ptr(), pid.data_ptr(), float(adv_eps),
+                                float(clip_eps), REDUCTIONS[reduction], lp.data_ptr(),
+                                lse.data_ptr(), adv.data_ptr(), dlp.data_ptr(), loss.data_ptr(),
+                                ws.data_ptr(), ws.numel(), stream_handle(dev)),
+          "grpo_fused_loss")
+    return {"loss": loss, "lp": lp, "lse": lse, "dlp": dlp, "adv": adv}
+
+
+def library_version() -> int:
+    return lib().qmi_version()

@@ -1,0 +1,74 @@
+"""The C-ABI library loads and exports every entry point include/qwen3mi.h declares
+(CPU: no kernel is launched here, only argument validation that returns
+before any HIP call)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "qwen3mi.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    names = re.findall(r"\b(qmi_\w+)\s*\(", text)
+    return sorted(set(names))
+
+
+def test_header_declares_entry_points():
+    names = declared_functions()
+    assert "qmi_store_kvcache" in names and "qmi_paged_decode_attention" in names
+    assert "qmi_grpo_fused_loss" in names
+
+
+def test_library_exports_every_declared_symbol(pkg):
+    handle = ctypes.CDLL(str(pkg._lib.LIB_PATH))
+    missing = [n for n in declared_functions() if not hasattr(handle, n)]
+    assert not missing, f"not exported: {missing}"
+
+
+def test_binding_table_covers_header(pkg):
+    assert set(declared_functions()) == set(pkg._lib.SIGNATURES)
+
+
+def test_error_strings_and_version(pkg):
+    L = pkg._lib.lib()
+    assert L.qmi_version() >= 100
+    assert L.qmi_error_string(0) == b"success"
+    assert b"NULL" in L.qmi_error_string(-1)
+    assert b"workspace" in L.qmi_error_string(-5)
+
+
+def test_validation_rejects_before_launch(pkg):
+    L = pkg._lib.lib()
+    # n_tokens == 0 is a no-op; negative sizes / NULL pointers are rejected.
+    assert L.qmi_store_kvcache(None, 1024, None, 1024, None, None, None, 0, 1024, 16, None) == 0
+    assert L.qmi_store_kvcache(None, 1024, None, 1024, None, None, None, 4, 1024, 16, None) == -1
+    assert L.qmi_store_kvcache(None, 1024, None, 1024, None, None, None, -1, 1024, 16, None) == -2
+    # unsupported head_dim / block size
+    fake = 256
+    st = L.qmi_paged_decode_attention(fake, 2048, 128, fake, fake, 16, 128, 16, 8, 128, fake, 1,
+                                      fake, 4, 4, 4, 0.1, fake, 2048, 128, None, 0, 0, None)
+    assert st == -4
+    # GQA ratio 3 is rejected
+    st = L.qmi_paged_decode_attention(fake, 2048, 128, fake, fake, 16, 256, 12, 4, 128, fake, 1,
+                                      fake, 4, 4, 4, 0.1, fake, 2048, 128, None, 0, 0, None)
+    assert st == -4
+    # workspace required when a sequence can need more than one split
+    need = L.qmi_paged_decode_workspace_bytes(4, 8, 16, 4, 1)
+    assert need == 4 * 16 * 4 * 132 * 4
+    st = L.qmi_paged_decode_attention(fake, 2048, 128, fake, fake, 16, 256, 16, 8, 128, fake, 1,
+                                      fake, 4, 4, 4, 0.1, fake, 2048, 128, None, 0, 1, None)
+    assert st == -5
+    assert L.qmi_grpo_fused_workspace_bytes(32, 512) >= 4 * 32 * 512
+    assert L.qmi_ppo_clipped_loss(None, None, None, None, 1, 0, 2, 3, 0.2, 0, None, None, None) == -1
+    assert L.qmi_ppo_clipped_loss(fake, fake, fake, fake, 1, 0, 2, 3, 0.2, 7, fake, None, None) == -4
+
+
+def test_product_fails_loudly_without_library(pkg, monkeypatch, tmp_path):
+    monkeypatch.setattr(pkg._lib, "_LIB", None)
+    monkeypatch.setattr(pkg._lib, "LIB_PATH", tmp_path / "missing.so")
+    with pytest.raises(pkg._lib.QmiError):
+        pkg._lib.lib()

@@ -1,0 +1,150 @@
+"""Paged decode attention parity against the oracle (tolerance: max abs 2e-2 in
+bf16, the bound the reference path is held to)."""
+import pytest
+import torch
+
+from oracle import attention as OA
+from oracle import paged as OP
+from oracle import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2
+
+
+def _decode(pkg, gpu, w, **kw):
+    return pkg.kernels.paged_decode_attention(
+        w["q"].to(gpu), w["k_cache"].to(gpu), w["v_cache"].to(gpu), w["cache_seqlens"].to(gpu),
+        w["block_tables"].to(gpu), w["scale"], **kw)
+
+
+def _check(out, w, tol=TOL):
+    ref = OA.paged_decode(w["q"].cpu(), w["k_cache"].cpu(), w["v_cache"].cpu(),
+                          w["cache_seqlens"].cpu(), w["block_tables"].cpu(), w["scale"])
+    err = (out.float().cpu() - ref).abs().max().item()
+    assert err <= tol, f"max abs err {err}"
+    return err
+
+
+def test_decode_config1_store_then_attend(pkg, gpu):
+    """Config 1 end to end: store the new K/V (bit-exact) then attend over ctx+1 keys."""
+    w = W.decode_one_layer(seed=0)
+    print("[decode] config1", flush=True)
+    kc, vc = w["k_cache"].to(gpu), w["v_cache"].to(gpu)
+    pkg.kernels.store_kvcache(w["k_new"].to(gpu), w["v_new"].to(gpu), kc, vc,
+                              w["slot_mapping"].to(gpu))
+    out = pkg.kernels.paged_decode_attention(
+        w["q"].to(gpu), kc, vc, w["context_lens"].to(gpu), w["block_tables"].to(gpu),
+        w["scale"], seqlen_bias=1)
+    torch.cuda.synchronize()
+    k_ref, v_ref = w["k_cache"].clone(), w["v_cache"].clone()
+    OP.store_kvcache(w["k_new"], w["v_new"], k_ref, v_ref, w["slot_mapping"])
+    assert torch.equal(kc.cpu(), k_ref) and torch.equal(vc.cpu(), v_ref)
+    w2 = dict(w, k_cache=k_ref, v_cache=v_ref)
+    _check(out, w2)
+    eager = OA.paged_decode(w["q"], k_ref, v_ref, w["cache_seqlens"], w["block_tables"],
+                            w["scale"], mode="bf16_eager")
+    assert (out.float().cpu() - eager).abs().max().item() <= TOL
+
+
+def _ragged(seed, lens, hq=16, hkv=8, extra=3):
+    g = torch.Generator().manual_seed(seed)
+    need = [max(1, (L + 255) // 256) for L in lens]
+    nb = sum(need) + extra
+    perm = torch.randperm(nb, generator=g)
+    width = max(need)
+    bt = torch.full((len(lens), width), -1, dtype=torch.int32)
+    off = 0
+    for b, n in enumerate(need):
+        bt[b, :n] = perm[off:off + n].to(torch.int32)
+        off += n
+    q = torch.randn(len(lens), hq, 128, generator=g).to(torch.bfloat16)
+    kc = torch.randn(nb, 256, hkv, 128, generator=g).to(torch.bfloat16)
+    vc = torch.randn(nb, 256, hkv, 128, generator=g).to(torch.bfloat16)
+    return dict(q=q, k_cache=kc, v_cache=vc, block_tables=bt,
+                cache_seqlens=torch.tensor(lens, dtype=torch.int32), scale=128 ** -0.5)
+
+
+@pytest.mark.parametrize("pps", [0, 1, 2, 3])
+def test_decode_page_boundaries_and_splits(pkg, gpu, pps):
+    lens = [1, 2, 255, 256, 257, 511, 512, 513, 1000, 1800]
+    w = _ragged(10 + pps, lens)
+    print(f"[decode] boundaries pps={pps}", flush=True)
+    out = _decode(pkg, gpu, w, pages_per_split=pps)
+    torch.cuda.synchronize()
+    _check(out, w)
+
+
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (16, 8), (16, 4), (32, 4)])
+def test_decode_gqa_ratios(pkg, gpu, hq, hkv):
+    w = _ragged(20 + hq + hkv, [37, 300, 700, 1025], hq=hq, hkv=hkv)
+    print(f"[decode] gqa {hq}/{hkv}", flush=True)
+    out = _decode(pkg, gpu, w, pages_per_split=1)
+    torch.cuda.synchronize()
+    _check(out, w)
+
+
+def test_decode_config3_shape(pkg, gpu):
+    """B=64, ctx ~ U{1024..4096}, shuffled tables: the serving-batch shape."""
+    w = W.decode_batch(seed=0, batch=64)
+    print("[decode] config3 shape", flush=True)
+    out = _decode(pkg, gpu, w, seqlen_bias=0)
+    torch.cuda.synchronize()
+    _check(out, w)
+
+
+def test_decode_zero_length_gives_zeros_and_strided_q(pkg, gpu):
+    w = _ragged(31, [0, 5, 300])
+    # q as a strided view of a fused projection: [B, 4096] -> first 2048 = 16 heads.
+    g = torch.Generator().manual_seed(32)
+    qkv = torch.randn(3, 4096, generator=g).to(torch.bfloat16)
+    w["q"] = qkv[:, :2048].view(3, 16, 128)
+    print("[decode] zero length + strided q", flush=True)
+    out = pkg.kernels.paged_decode_attention(
+        qkv.to(gpu)[:, :2048].view(3, 16, 128), w["k_cache"].to(gpu), w["v_cache"].to(gpu),
+        w["cache_seqlens"].to(gpu), w["block_tables"].to(gpu), w["scale"])
+    torch.cuda.synchronize()
+    assert out[0].abs().max().item() == 0.0
+    _check(out, w)
+
+
+def test_decode_graph_replay_matches_eager(pkg, gpu):
+    """Capturable: replay with new inputs copied into static buffers."""
+    w = _ragged(40, [100, 700, 1300, 260])
+    q = w["q"].to(gpu)
+    kc, vc = w["k_cache"].to(gpu), w["v_cache"].to(gpu)
+    lens = w["cache_seqlens"].to(gpu)
+    bt = w["block_tables"].to(gpu)
+    print("[decode] graph capture", flush=True)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        pkg.kernels.paged_decode_attention(q, kc, vc, lens, bt, w["scale"])  # warm-up
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = pkg.kernels.paged_decode_attention(q, kc, vc, lens, bt, w["scale"])
+    g = torch.Generator().manual_seed(41)
+    for it in range(4):
+        q.copy_(torch.randn(q.shape, generator=g).to(torch.bfloat16))
+        lens.copy_(torch.tensor([100 + it * 40, 700 - it, 1300 - 300 * it, 5 + it], dtype=torch.int32))
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = pkg.kernels.paged_decode_attention(q, kc, vc, lens, bt, w["scale"])
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        _check(out, dict(w, q=q.cpu(), cache_seqlens=lens.cpu()))
+
+
+def test_decode_rejects_bad_shapes(pkg, gpu):
+    w = _ragged(50, [10])
+    q = w["q"].to(gpu)
+    with pytest.raises(ValueError):
+        pkg.kernels.paged_decode_attention(q[:, :, :64], w["k_cache"].to(gpu),
+                                           w["v_cache"].to(gpu), w["cache_seqlens"].to(gpu),
+                                           w["block_tables"].to(gpu), 0.1)
+    with pytest.raises(ValueError):
+        pkg.kernels.paged_decode_attention(q, w["k_cache"].to(gpu)[:, :128].contiguous(),
+                                           w["v_cache"].to(gpu)[:, :128].contiguous(),
+                                           w["cache_seqlens"].to(gpu), w["block_tables"].to(gpu),
+                                           0.1)
