@@ -124,7 +124,7 @@ int qmi_grpo_advantage(const float* rewards, const int64_t* prompt_ids, int64_t 
                        float eps, float* out_adv, void* stream);
 
 #define QMI_REDUCE_TOKEN_MEAN 0   /* sum(l*m) / (sum(m) + 1e-8), qwen3_grpo_train.py:198 */
-#define QMI_REDUCE_SEQ_MEAN 1     /* mean_b( sum_t(l*m) / sum_t(m) ) */
+#define QMI_REDUCE_SEQ_MEAN 1     /* mean_b( sum_t(l*m) / (sum_t(m) + 1e-8) ) */
 
 /*
  * PPO clipped surrogate on given log-probabilities.
@@ -156,8 +156,10 @@ int qmi_ppo_clipped_loss(const float* new_lp, const float* old_lp, const float* 
  * contiguous; rewards fp32 [n_seq]; prompt_ids int64 [n_seq].
  * Outputs: out_lp, out_lse fp32 [n_seq, n_tok]; out_adv fp32 [n_seq];
  * out_dlp fp32 [n_seq, n_tok] (d loss / d lp); out_loss fp32 scalar.
- * workspace: qmi_grpo_fused_workspace_bytes(n_seq, n_tok) bytes, zeroed
- * by the caller once before first use; the kernels leave it zeroed again.
+ * workspace: qmi_grpo_fused_workspace_bytes(n_seq, n_tok) bytes (arrival
+ * counters and per-sequence sums), zeroed by the caller once before first
+ * use; the kernel leaves its counters at zero again when it completes, so
+ * calls on one stream can reuse it.  Concurrent calls must not share one.
  */
 int64_t qmi_grpo_fused_workspace_bytes(int64_t n_seq, int64_t n_tok);
 

@@ -12,12 +12,14 @@
 // 32x512x151936 loss step) is the whole cost, so one workgroup streams one
 // row with dwordx4 non-temporal loads, four chunks in flight per lane, and
 // keeps a per-lane (max, sum of exp2) pair rescaled once per 32 elements.
-// The pairs are merged with shuffles and one LDS exchange.  The fused
-// kernel finishes the loss in-kernel: each row writes its masked token
-// loss and d loss / d lp; the last row of every sequence (an atomic arrival
-// counter) sums that sequence and normalises its gradients; the last
-// sequence sums the sequences.  All sums run in a fixed order, so results
-// are deterministic, and the counters are reset by the finishers.
+// The pairs are merged with shuffles and one LDS exchange.  Row workgroups
+// use no fences or atomics: an agent-scope fence on gfx950 writes back and
+// invalidates the L2, which costs more than the row itself when 16K
+// workgroups each issue one.  The loss therefore runs as a second, tiny
+// launch with one workgroup per sequence (advantage, token losses and their
+// gradients), whose last arrival computes the scalar.  All sums run in a
+// fixed order, so results are deterministic; the arrival counter is reset by
+// the finisher.
 #include "qmi_common.h"
 
 namespace {
@@ -151,6 +153,13 @@ __device__ __forceinline__ void ppo_token(float new_lp, float old_lp, float adv,
 }
 
 // ---------------------------------------------------------------------------
+// Lane 0's gathered logit for the row's token.  Issued before the streaming
+// loop so its latency overlaps the row read instead of trailing it.
+__device__ __forceinline__ float gather_token_logit(const uint16_t* __restrict__ rp, int64_t id,
+                                                    int64_t vocab) {
+  return (id >= 0 && id < vocab) ? bf16_to_f32(rp[id]) : __builtin_nanf("");
+}
+
 template <bool VEC>
 __global__ __launch_bounds__(kThreads) void logprob_rows(
     const uint16_t* __restrict__ logits, int64_t lss, int64_t lts,
@@ -160,42 +169,36 @@ __global__ __launch_bounds__(kThreads) void logprob_rows(
   const int64_t row = blockIdx.x;
   const int64_t b = row / n_tok, t = row - b * n_tok;
   const uint16_t* rp = logits + b * lss + t * lts;
-  const int64_t id = ids[b * iss + t * its];
+  float xid = 0.f;
+  if (threadIdx.x == 0) xid = gather_token_logit(rp, ids[b * iss + t * its], vocab);
   const float lse2 = row_lse2<VEC>(rp, vocab, sm_m, sm_s);
   if (threadIdx.x == 0) {
     const float lse = lse2 * kLn2;
-    const float xid = (id >= 0 && id < vocab) ? bf16_to_f32(rp[id]) : __builtin_nanf("");
     out_lp[row] = xid - lse;
     if (out_lse) out_lse[row] = lse;
   }
 }
 
 struct FusedWs {
-  uint32_t* seq_count;   // [n_seq]
-  uint32_t* all_count;   // [1]
-  float* seq_sum;        // [n_seq]  sum_t l*m
-  float* seq_msum;       // [n_seq]  sum_t m
-  float* tok_loss;       // [n_seq * n_tok]
+  uint32_t* all_count;   // [1]     sequences that have finished
+  float* seq_sum;        // [n_seq] sum_t l*m
+  float* seq_msum;       // [n_seq] sum_t m
 };
 
 __host__ __device__ inline int64_t align16(int64_t x) { return (x + 15) & ~(int64_t)15; }
 
-__host__ __device__ inline int64_t fused_ws_bytes(int64_t n_seq, int64_t n_tok) {
-  return align16(4 * n_seq) + align16(4) + 2 * align16(4 * n_seq) + align16(4 * n_seq * n_tok);
+__host__ __device__ inline int64_t fused_ws_bytes(int64_t n_seq) {
+  return align16(4) + 2 * align16(4 * n_seq);
 }
 
-__device__ inline FusedWs fused_ws(void* base, int64_t n_seq, int64_t n_tok) {
+__device__ inline FusedWs fused_ws(void* base, int64_t n_seq) {
   char* p = reinterpret_cast<char*>(base);
   FusedWs w;
-  w.seq_count = reinterpret_cast<uint32_t*>(p);
-  p += align16(4 * n_seq);
   w.all_count = reinterpret_cast<uint32_t*>(p);
   p += align16(4);
   w.seq_sum = reinterpret_cast<float*>(p);
   p += align16(4 * n_seq);
   w.seq_msum = reinterpret_cast<float*>(p);
-  p += align16(4 * n_seq);
-  w.tok_loss = reinterpret_cast<float*>(p);
   return w;
 }
 
@@ -212,6 +215,32 @@ __device__ float block_sum(float x, float* sm) {
   return t;
 }
 
+// Group advantage of sequence i computed by the whole block (parallel scan of
+// the prompt ids; two fixed-order block reductions).
+__device__ float block_group_advantage(const float* __restrict__ rewards,
+                                       const int64_t* __restrict__ prompt_ids, int64_t n,
+                                       int64_t i, float eps, float* sm) {
+  const int64_t pid = prompt_ids[i];
+  float sum = 0.f, cnt = 0.f;
+  for (int64_t j = threadIdx.x; j < n; j += kThreads)
+    if (prompt_ids[j] == pid) {
+      sum += rewards[j];
+      cnt += 1.f;
+    }
+  sum = block_sum(sum, sm);
+  cnt = block_sum(cnt, sm);
+  const float mean = sum / cnt;
+  float ss = 0.f;
+  for (int64_t j = threadIdx.x; j < n; j += kThreads)
+    if (prompt_ids[j] == pid) {
+      const float d = rewards[j] - mean;
+      ss += d * d;
+    }
+  ss = block_sum(ss, sm);
+  // Unbiased estimate; a group of one gives 0/0 = NaN exactly as torch.std().
+  return (rewards[i] - mean) / (sqrtf(ss / (cnt - 1.f)) + eps);
+}
+
 __device__ __forceinline__ uint32_t arrive(uint32_t* counter) {
   return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -220,71 +249,60 @@ __device__ __forceinline__ void reset_counter(uint32_t* counter) {
   __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <bool VEC>
-__global__ __launch_bounds__(kThreads) void grpo_fused_rows(
-    const uint16_t* __restrict__ logits, int64_t lss, int64_t lts,
-    const int64_t* __restrict__ ids, int64_t iss, int64_t its, int64_t n_seq, int64_t n_tok,
-    int64_t vocab, const float* __restrict__ old_lp, const float* __restrict__ mask,
-    const float* __restrict__ rewards, const int64_t* __restrict__ prompt_ids, float adv_eps,
-    float clip, int reduction, float* __restrict__ out_lp, float* __restrict__ out_lse,
-    float* __restrict__ out_adv, float* __restrict__ out_dlp, float* __restrict__ out_loss,
-    void* __restrict__ ws_base) {
-  __shared__ float sm_m[kWaves], sm_s[kWaves], sm_red[kWaves];
+// Loss epilogue of the fused step, launched right after logprob_rows has
+// written lp for every row (the kernel boundary orders the two, so the row
+// workgroups need no fences or atomics).  One workgroup per sequence b: the
+// group advantage of b, the masked token losses and their gradients for the
+// n_tok tokens of b, and b's sums.  The last sequence to finish (an arrival
+// counter; n_seq fences in total) computes the scalar loss.  Every reduction
+// runs in a fixed order, so the result is deterministic.
+__global__ __launch_bounds__(kThreads) void grpo_loss_seqs(
+    const float* __restrict__ lp, const float* __restrict__ old_lp,
+    const float* __restrict__ mask, const float* __restrict__ rewards,
+    const int64_t* __restrict__ prompt_ids, int64_t n_seq, int64_t n_tok, float adv_eps,
+    float clip, int reduction, float* __restrict__ out_adv, float* __restrict__ out_dlp,
+    float* __restrict__ out_loss, void* __restrict__ ws_base) {
+  __shared__ float sm_red[kWaves];
   __shared__ bool sm_last;
-  const FusedWs ws = fused_ws(ws_base, n_seq, n_tok);
-  const int64_t row = blockIdx.x;
-  const int64_t b = row / n_tok, t = row - b * n_tok;
-  const uint16_t* rp = logits + b * lss + t * lts;
-  const int64_t id = ids[b * iss + t * its];
-  const float lse2 = row_lse2<VEC>(rp, vocab, sm_m, sm_s);
-
-  if (threadIdx.x == 0) {
-    const float lse = lse2 * kLn2;
-    const float xid = (id >= 0 && id < vocab) ? bf16_to_f32(rp[id]) : __builtin_nanf("");
-    const float lp = xid - lse;
-    out_lp[row] = lp;
-    out_lse[row] = lse;
-    const float m = mask[row];
-    float tl = 0.f, tg = 0.f;
-    if (m != 0.f) {
-      const float adv = group_advantage(rewards, prompt_ids, n_seq, b, adv_eps);
-      float l, g;
-      ppo_token(lp, old_lp[row], adv, clip, &l, &g);
-      tl = l * m;
-      tg = g * m;
-    }
-    ws.tok_loss[row] = tl;
-    out_dlp[row] = tg;  // normalised by the sequence finisher below
-    __threadfence();
-    sm_last = (arrive(&ws.seq_count[b]) == (uint32_t)(n_tok - 1));
-  }
-  __syncthreads();
-  if (!sm_last) return;
-
-  // ---- last row of sequence b: per-sequence sums and gradient scaling ----
-  __threadfence();
-  float sl = 0.f, sm = 0.f;
+  const FusedWs ws = fused_ws(ws_base, n_seq);
+  const int64_t b = blockIdx.x;
+  const float adv = block_group_advantage(rewards, prompt_ids, n_seq, b, adv_eps, sm_red);
+  const int64_t base = b * n_tok;
+  float sl = 0.f, smk = 0.f;
   for (int64_t j = threadIdx.x; j < n_tok; j += kThreads) {
-    sl += ws.tok_loss[b * n_tok + j];
-    sm += mask[b * n_tok + j];
+    const float m = mask[base + j];
+    smk += m;
+    if (m != 0.f) {
+      float l, g;
+      ppo_token(lp[base + j], old_lp[base + j], adv, clip, &l, &g);
+      sl += l * m;
+    }
   }
   sl = block_sum(sl, sm_red);
-  sm = block_sum(sm, sm_red);
+  smk = block_sum(smk, sm_red);
   float den;
   if (reduction == QMI_REDUCE_TOKEN_MEAN) {
     float all = 0.f;
     for (int64_t j = threadIdx.x; j < n_seq * n_tok; j += kThreads) all += mask[j];
     den = block_sum(all, sm_red) + 1e-8f;
   } else {
-    den = (float)n_seq * (sm + 1e-8f);
+    den = (float)n_seq * (smk + 1e-8f);
   }
   const float inv = 1.0f / den;
-  for (int64_t j = threadIdx.x; j < n_tok; j += kThreads) out_dlp[b * n_tok + j] *= inv;
+  for (int64_t j = threadIdx.x; j < n_tok; j += kThreads) {
+    const float m = mask[base + j];
+    float g = 0.f;
+    if (m != 0.f) {
+      float l;
+      ppo_token(lp[base + j], old_lp[base + j], adv, clip, &l, &g);
+      g *= m * inv;
+    }
+    out_dlp[base + j] = g;
+  }
   if (threadIdx.x == 0) {
     ws.seq_sum[b] = sl;
-    ws.seq_msum[b] = sm;
-    out_adv[b] = group_advantage(rewards, prompt_ids, n_seq, b, adv_eps);
-    reset_counter(&ws.seq_count[b]);
+    ws.seq_msum[b] = smk;
+    out_adv[b] = adv;
     __threadfence();
     sm_last = (arrive(ws.all_count) == (uint32_t)(n_seq - 1));
   }
@@ -490,7 +508,7 @@ extern "C" int qmi_ppo_clipped_loss(const float* new_lp, const float* old_lp, co
 
 extern "C" int64_t qmi_grpo_fused_workspace_bytes(int64_t n_seq, int64_t n_tok) {
   if (n_seq <= 0 || n_tok <= 0) return 0;
-  return fused_ws_bytes(n_seq, n_tok);
+  return fused_ws_bytes(n_seq);
 }
 
 extern "C" int qmi_grpo_fused_loss(const uint16_t* logits, int64_t lss, int64_t lts,
@@ -508,20 +526,21 @@ extern "C" int qmi_grpo_fused_loss(const uint16_t* logits, int64_t lss, int64_t 
   if (reduction != QMI_REDUCE_TOKEN_MEAN && reduction != QMI_REDUCE_SEQ_MEAN)
     return QMI_E_UNSUPPORTED;
   if (n_seq * n_tok > 0x7fffffffLL) return QMI_E_UNSUPPORTED;
-  if (workspace_bytes < fused_ws_bytes(n_seq, n_tok)) return QMI_E_WORKSPACE_TOO_SMALL;
+  if (workspace_bytes < fused_ws_bytes(n_seq)) return QMI_E_WORKSPACE_TOO_SMALL;
   if (reinterpret_cast<uintptr_t>(workspace) & 15u) return QMI_E_BAD_STRIDE;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)(n_seq * n_tok));
   if (rows_vec_ok(logits, lss, lts))
-    hipLaunchKernelGGL(grpo_fused_rows<true>, grid, dim3(kThreads), 0, s, logits, lss, lts, ids,
-                       iss, its, n_seq, n_tok, vocab, old_lp, mask, rewards, prompt_ids, adv_eps,
-                       clip_eps, (int)reduction, out_lp, out_lse, out_adv, out_dlp, out_loss,
-                       workspace);
+    hipLaunchKernelGGL(logprob_rows<true>, grid, dim3(kThreads), 0, s, logits, lss, lts, ids, iss,
+                       its, n_tok, vocab, out_lp, out_lse);
   else
-    hipLaunchKernelGGL(grpo_fused_rows<false>, grid, dim3(kThreads), 0, s, logits, lss, lts, ids,
-                       iss, its, n_seq, n_tok, vocab, old_lp, mask, rewards, prompt_ids, adv_eps,
-                       clip_eps, (int)reduction, out_lp, out_lse, out_adv, out_dlp, out_loss,
-                       workspace);
+    hipLaunchKernelGGL(logprob_rows<false>, grid, dim3(kThreads), 0, s, logits, lss, lts, ids,
+                       iss, its, n_tok, vocab, out_lp, out_lse);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL(grpo_loss_seqs, dim3((unsigned)n_seq), dim3(kThreads), 0, s, out_lp, old_lp,
+                     mask, rewards, prompt_ids, n_seq, n_tok, adv_eps, clip_eps, (int)reduction,
+                     out_adv, out_dlp, out_loss, workspace);
   QMI_RETURN_LAUNCH_STATUS();
 }
 
