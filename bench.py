@@ -9,10 +9,11 @@ in total), so the 256 MB Infinity Cache cannot serve the reads.  A "step" is
 the 28 decode-attention launches of one decode step.
 
 Secondary legs (same JSON line): the fused GRPO logprob+advantage+loss kernel
-on the 32x512x151936 loss step, the KV store at 65,536 tokens, and the CPU
+on the 32x512x151936 loss step, the KV store at 65,536 tokens, the varlen
+paged prefill on the prefix-cache chunk workload (MFMA TFLOP/s), and the CPU
 oracle (the CPU restatement of the reference semantics) timed on this host.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--legs decode,grpo,store]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--legs decode,grpo,store,prefill]
        [--no-cpu] [--calibrate-copy]
 """
 from __future__ import annotations
@@ -31,6 +32,7 @@ if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 METRIC = "decode-attn HBM GB/s (% of 8 TB/s); GRPO rollout tokens/s on 1 GPU"
 
 
@@ -141,6 +143,32 @@ def leg_store(torch, pkg, dev, steps, warmup, n_tok=65536):
                 tokens=n_tok)
 
 
+def leg_prefill(torch, pkg, W, dev, steps, warmup):
+    """Config 4: one layer's attention over every chunk step of the prefix-cache
+    workload (16 sequences, 512-token shared prefix, suffixes U{256..2048} in
+    512-token chunks).  Algorithmic FLOPs count unmasked (query, key) pairs."""
+    sched = W.prefix_prefill_chunks(seed=0)
+    n_blocks = 2 + 16 * 16
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    kc = torch.randn((n_blocks, 256, 8, 128), generator=g, device=dev).to(torch.bfloat16)
+    vc = torch.randn((n_blocks, 256, 8, 128), generator=g, device=dev).to(torch.bfloat16)
+    calls, pairs = [], 0
+    for i, step in enumerate(sched["steps"]):
+        inp = W.prefill_step_inputs(i, step, [0, 1], n_blocks, device=dev)
+        pairs += W.causal_pairs(inp["cu_seqlens_q"].tolist(), inp["cu_seqlens_k"].tolist())
+        calls.append(inp)
+    flops = 4 * 16 * 128 * pairs
+    fns = [(lambda c=c: pkg.kernels.varlen_prefill_attention(
+        c["q"], kc, vc, c["cu_seqlens_q"], c["cu_seqlens_k"], c["max_seqlen_q"],
+        c["max_seqlen_k"], 128 ** -0.5, True, c["block_tables"])) for c in calls]
+    total_ms, per = timed_launches(torch, fns, steps, warmup)
+    ms = total_ms / steps
+    return dict(ms_per_layer=ms, tflops=flops / (ms * 1e-3) / 1e12, flops=flops,
+                causal_pairs=pairs, n_steps=len(calls),
+                q_tokens=sum(int(c["cu_seqlens_q"][-1]) for c in calls))
+
+
 def leg_copy_calibration(torch, dev, nbytes=1 << 30):
     """A plain device copy of known size, for scaling FETCH_SIZE / WRITE_SIZE."""
     src = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=dev).fill_(1)
@@ -214,7 +242,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--legs", default="decode,grpo,store")
+    ap.add_argument("--legs", default="decode,grpo,store,prefill")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 1 GiB device copy (counter calibration)")
@@ -247,6 +275,8 @@ def main() -> int:
         results["grpo"] = leg_grpo(torch, pkg, W, dev, max(3, args.steps // 2), args.warmup)
     if "store" in legs:
         results["store"] = leg_store(torch, pkg, dev, args.steps, args.warmup)
+    if "prefill" in legs:
+        results["prefill"] = leg_prefill(torch, pkg, W, dev, max(3, args.steps // 2), args.warmup)
 
     cpu = None
     if not args.no_cpu and "decode" in results:
@@ -274,6 +304,16 @@ def main() -> int:
             "us_per_launch": round(r["avg_launch_us"], 2), "gbs": round(r["gbs"], 1),
             "frac_of_hbm_peak": round(r["gbs"] / HBM_PEAK_GBS, 4),
             "bytes_per_launch": r["bytes_per_launch"]}
+
+    if "prefill" in results:
+        r = results["prefill"]
+        secondary["prefill_attention"] = {
+            "workload": "varlen paged causal prefill, 16 seqs sharing a cached 512-token prefix, "
+                        "suffixes U{256..2048} in 512-token chunks, one layer (all chunk steps)",
+            "ms_per_layer": round(r["ms_per_layer"], 4), "tflops": round(r["tflops"], 1),
+            "frac_of_bf16_mfma_peak": round(r["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4),
+            "flops_per_layer": r["flops"], "causal_pairs": r["causal_pairs"],
+            "chunk_steps": r["n_steps"], "query_tokens": r["q_tokens"]}
 
     if "decode" in results:
         d = results["decode"]

@@ -94,6 +94,34 @@ int qmi_paged_decode_attention(const uint16_t* q, int64_t q_seq_stride, int64_t 
                                int64_t pages_per_split, void* stream);
 
 /*
+ * Varlen paged causal prefill attention (bf16 MFMA).
+ * Replaces `flash_attn_varlen_func(q, k_cache, v_cache, cu_seqlens_q,
+ * cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale, causal=True,
+ * block_table=block_tables)` in Qwen3Attention.forward_prefill
+ * (qwen3_naive.py:631-637).
+ *
+ * q   : [total_q, num_q_heads, head_dim] bf16 (element strides; unit stride
+ *       along head_dim); out has the same shape and its own strides.
+ * Sequence b owns query rows cu_seqlens_q[b] .. cu_seqlens_q[b+1]-1 and
+ * Lk = cu_seqlens_k[b+1] - cu_seqlens_k[b] keys, all already stored in the
+ * paged caches (key j at row j % 256 of page block_table[b, j / 256]).
+ * Causal masking is bottom-right aligned: query i of the Lq new ones sees
+ * keys j <= i + Lk - Lq (new tokens see the whole cached prefix).
+ * max_seqlen_q bounds Lq (it sizes the grid).  Query rows outside
+ * [0, total_q) are never read or written.  Supported: head_dim 128,
+ * block_size 256, num_q_heads / num_kv_heads in {1, 2, 4}.
+ */
+int qmi_varlen_prefill_attention(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride,
+                                 const uint16_t* k_cache, const uint16_t* v_cache,
+                                 int64_t num_blocks, int64_t block_size,
+                                 int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                                 const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                 const int32_t* block_table, int64_t bt_stride, int64_t bt_width,
+                                 int64_t batch, int64_t max_seqlen_q, int64_t total_q, float scale,
+                                 uint16_t* out, int64_t out_tok_stride, int64_t out_head_stride,
+                                 void* stream);
+
+/*
  * Row-wise log-softmax gathered at one token per row.
  * Replaces `F.log_softmax(logits.float(), -1).gather(-1, ids)` of
  * forward_logprob (qwen3_grpo_train.py:46-53) and the rollout's

@@ -149,6 +149,74 @@ def paged_decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
 
 
 # ---------------------------------------------------------------------------
+# Varlen paged causal prefill (flash_attn_varlen_func at qwen3_naive.py:631-637)
+# ---------------------------------------------------------------------------
+def varlen_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                             cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor,
+                             max_seqlen_q: int, max_seqlen_k: int, softmax_scale: float,
+                             causal: bool = True, block_table: torch.Tensor | None = None,
+                             out: torch.Tensor | None = None) -> torch.Tensor:
+    """Varlen causal attention of the new tokens over their paged K/V.
+
+    Argument order and meaning follow the reference call
+    ``flash_attn_varlen_func(q, k_cache, v_cache, max_seqlen_q=..., cu_seqlens_q=...,
+    max_seqlen_k=..., cu_seqlens_k=..., softmax_scale=..., causal=True,
+    block_table=...)``.  ``q``: ``[Tq, Hq, 128]`` bf16; caches
+    ``[num_blocks, 256, Hkv, 128]``; ``cu_seqlens_*``: int32 ``[B+1]``;
+    ``block_table``: int32 ``[B, W]``.  Returns ``[Tq, Hq, 128]`` bf16.
+    ``max_seqlen_k`` is accepted for signature parity (the kernel reads the
+    per-sequence key counts from ``cu_seqlens_k``).
+    """
+    if not causal:
+        raise ValueError("only causal=True is supported (the reference always passes it)")
+    if block_table is None:
+        raise ValueError("block_table is required: keys are always read from the paged cache")
+    for n, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache)):
+        _require_cuda(n, t)
+        _require_dtype(n, t, torch.bfloat16)
+    if q.dim() != 3:
+        raise ValueError(f"q must be [Tq, Hq, D], got {tuple(q.shape)}")
+    tq, hq, d = q.shape
+    if k_cache.dim() != 4 or k_cache.shape != v_cache.shape:
+        raise ValueError("caches must be [num_blocks, block_size, Hkv, D] of equal shape")
+    nb, bs, hkv, dk = k_cache.shape
+    if d != HEAD_DIM or dk != HEAD_DIM or bs != BLOCK_SIZE:
+        raise ValueError(f"supported: head_dim {HEAD_DIM}, block_size {BLOCK_SIZE}")
+    if hq % hkv != 0 or (hq // hkv) not in (1, 2, 4):
+        raise ValueError(f"GQA ratio Hq/Hkv must be 1, 2 or 4 (Hq={hq}, Hkv={hkv})")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("caches must be contiguous")
+    if q.stride(2) != 1 or q.stride(0) % 8 or q.stride(1) % 8:
+        q = q.contiguous()
+    cq = _as_i32("cu_seqlens_q", cu_seqlens_q).contiguous()
+    ck = _as_i32("cu_seqlens_k", cu_seqlens_k).contiguous()
+    bt = _as_i32("block_table", block_table)
+    if cq.dim() != 1 or ck.shape != cq.shape or cq.shape[0] < 1:
+        raise ValueError("cu_seqlens_q / cu_seqlens_k must both be [B+1]")
+    bsz = cq.shape[0] - 1
+    if bt.dim() != 2 or bt.shape[0] != bsz or bt.shape[1] < 1:
+        raise ValueError(f"block_table must be [{bsz}, W>=1], got {tuple(bt.shape)}")
+    if bt.stride(1) != 1:
+        bt = bt.contiguous()
+    if out is None:
+        out = torch.empty((tq, hq, d), dtype=torch.bfloat16, device=q.device)
+    else:
+        _require_cuda("out", out)
+        _require_dtype("out", out, torch.bfloat16)
+        if out.shape != (tq, hq, d) or out.stride(2) != 1:
+            raise ValueError("out must be [Tq, Hq, D] with unit stride along D")
+    if bsz == 0 or tq == 0 or int(max_seqlen_q) == 0:
+        return out
+    st = lib().qmi_varlen_prefill_attention(
+        q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(), nb, bs,
+        hq, hkv, d, cq.data_ptr(), ck.data_ptr(), bt.data_ptr(), bt.stride(0), bt.shape[1], bsz,
+        int(max_seqlen_q), tq, float(softmax_scale), out.data_ptr(), out.stride(0), out.stride(1),
+        stream_handle(q.device))
+    check(st, "varlen_prefill_attention")
+    return out
+
+
+# ---------------------------------------------------------------------------
 # Log-softmax gather (qwen3_grpo_train.py:46-53)
 # ---------------------------------------------------------------------------
 def _rows_view(logits: torch.Tensor, ids: torch.Tensor):
