@@ -122,6 +122,51 @@ int qmi_varlen_prefill_attention(const uint16_t* q, int64_t q_tok_stride, int64_
                                  void* stream);
 
 /*
+ * RMSNorm over rows of n bf16 elements with bf16 weight[n]:
+ *   y = bf16(x * rsqrt(mean(x^2) + eps) * w), all math in fp32.
+ * Replaces RMSNorm._rms_norm (qwen3_naive.py:156-161).  n % 8 == 0, n <= 4096.
+ */
+int qmi_rms_norm(const uint16_t* x, int64_t x_stride, const uint16_t* weight, uint16_t* y,
+                 int64_t y_stride, int64_t n_rows, int64_t n, float eps, void* stream);
+
+/*
+ * Fused residual add + RMSNorm.  Replaces RMSNorm._add_rms_norm
+ * (qwen3_naive.py:163-169): s = x + residual (fp32); residual_out = bf16(s);
+ * y = bf16(s * rsqrt(mean(s^2) + eps) * w).  residual_out may alias residual.
+ */
+int qmi_add_rms_norm(const uint16_t* x, int64_t x_stride, const uint16_t* residual,
+                     int64_t residual_stride, uint16_t* residual_out, int64_t residual_out_stride,
+                     const uint16_t* weight, uint16_t* y, int64_t y_stride, int64_t n_rows,
+                     int64_t n, float eps, void* stream);
+
+/*
+ * Fused per-head QK-RMSNorm + RoPE on the fused qkv projection.
+ * Replaces q_norm / k_norm (qwen3_naive.py:661-662, RMSNorm over head_dim)
+ * followed by RotaryEmbedding / _apply_rope_kernel (qwen3_naive.py:44-80,
+ * :390-404).  qkv: [n_tok, (Hq + 2*Hkv) * 128] bf16 rows (q heads, then k
+ * heads, then v heads).  For every q and k head: RMSNorm with the bf16
+ * weight (rounded to bf16 as the reference does), then the half-split
+ * rotation with cos/sin from the fp32 cos_sin_cache[max_position, 128]
+ * (first 64 columns cos, last 64 sin) at positions[tok] (int64, clamped to
+ * [0, max_position)).  Writes q_out [n_tok, Hq, 128] and k_out
+ * [n_tok, Hkv, 128] (row strides q_stride / k_stride).  head_dim 128 only.
+ */
+int qmi_qk_norm_rope(const uint16_t* qkv, int64_t qkv_stride, int64_t n_tok, int64_t num_q_heads,
+                     int64_t num_kv_heads, int64_t head_dim, const uint16_t* q_norm_weight,
+                     const uint16_t* k_norm_weight, const int64_t* positions,
+                     const float* cos_sin_cache, int64_t max_position, uint16_t* q_out,
+                     int64_t q_stride, uint16_t* k_out, int64_t k_stride, float eps,
+                     void* stream);
+
+/*
+ * SwiGLU activation of the fused gate_up projection.  Replaces
+ * `silu(gate) * up` of Qwen3MLP.forward (qwen3_naive.py:695-702):
+ * out[r, j] = bf16(silu(g) * u) with g = gate_up[r, j], u = gate_up[r, inter + j].
+ */
+int qmi_silu_mul(const uint16_t* gate_up, int64_t gate_up_stride, int64_t n_rows, int64_t inter,
+                 uint16_t* out, int64_t out_stride, void* stream);
+
+/*
  * Row-wise log-softmax gathered at one token per row.
  * Replaces `F.log_softmax(logits.float(), -1).gather(-1, ids)` of
  * forward_logprob (qwen3_grpo_train.py:46-53) and the rollout's

@@ -44,6 +44,14 @@ SIGNATURES: dict[str, tuple] = {
         _c_p, _c_i64, _c_i64,            # block_table, stride, width
         _c_i64, _c_i64, _c_i64, _c_f32,  # batch, max_seqlen_q, total_q, scale
         _c_p, _c_i64, _c_i64, _c_p]),    # out, strides, stream
+    "qmi_rms_norm": (ctypes.c_int, [_c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_f32,
+                                    _c_p]),
+    "qmi_add_rms_norm": (ctypes.c_int, [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p,
+                                        _c_i64, _c_i64, _c_i64, _c_f32, _c_p]),
+    "qmi_qk_norm_rope": (ctypes.c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p,
+                                        _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_i64, _c_f32,
+                                        _c_p]),
+    "qmi_silu_mul": (ctypes.c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p]),
     "qmi_logprob_gather": (ctypes.c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i64,
                                           _c_i64, _c_i64, _c_p, _c_p, _c_p]),
     "qmi_grpo_advantage": (ctypes.c_int, [_c_p, _c_p, _c_i64, _c_f32, _c_p, _c_p]),

@@ -217,6 +217,92 @@ def varlen_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: to
 
 
 # ---------------------------------------------------------------------------
+# RMSNorm / QK-norm + RoPE / SwiGLU (qwen3_naive.py:44-80, :156-169, :695-702)
+# ---------------------------------------------------------------------------
+def _rows2d(name: str, x: torch.Tensor) -> torch.Tensor:
+    _require_cuda(name, x)
+    _require_dtype(name, x, torch.bfloat16)
+    x2 = x.reshape(-1, x.shape[-1])
+    if x2.stride(1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    return x2
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """``bf16(x * rsqrt(mean(x^2) + eps) * w)`` over the last dim (fp32 math)."""
+    x2 = _rows2d("x", x)
+    w = weight.to(torch.bfloat16).contiguous()
+    y = torch.empty(x2.shape, dtype=torch.bfloat16, device=x2.device)
+    check(lib().qmi_rms_norm(x2.data_ptr(), x2.stride(0), w.data_ptr(), y.data_ptr(), y.stride(0),
+                             x2.shape[0], x2.shape[1], float(eps), stream_handle(x2.device)),
+          "rms_norm")
+    return y.view(x.shape)
+
+
+def add_rms_norm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float):
+    """``s = x + residual``; returns ``(rms_norm(s), bf16(s))`` (fused)."""
+    x2 = _rows2d("x", x)
+    r2 = _rows2d("residual", residual)
+    if r2.shape != x2.shape:
+        raise ValueError("x and residual must have the same shape")
+    w = weight.to(torch.bfloat16).contiguous()
+    y = torch.empty(x2.shape, dtype=torch.bfloat16, device=x2.device)
+    r_out = torch.empty_like(y)
+    check(lib().qmi_add_rms_norm(x2.data_ptr(), x2.stride(0), r2.data_ptr(), r2.stride(0),
+                                 r_out.data_ptr(), r_out.stride(0), w.data_ptr(), y.data_ptr(),
+                                 y.stride(0), x2.shape[0], x2.shape[1], float(eps),
+                                 stream_handle(x2.device)),
+          "add_rms_norm")
+    return y.view(x.shape), r_out.view(x.shape)
+
+
+def qk_norm_rope(qkv: torch.Tensor, q_norm_weight: torch.Tensor, k_norm_weight: torch.Tensor,
+                 positions: torch.Tensor, cos_sin_cache: torch.Tensor, num_q_heads: int,
+                 num_kv_heads: int, eps: float):
+    """Per-head RMSNorm of q and k followed by half-split RoPE, from fused qkv rows.
+
+    ``qkv``: ``[N, (Hq + 2 Hkv) * 128]`` bf16.  Returns contiguous
+    ``q [N, Hq, 128]`` and ``k [N, Hkv, 128]``; v stays a view of ``qkv``.
+    """
+    _require_cuda("qkv", qkv)
+    _require_dtype("qkv", qkv, torch.bfloat16)
+    if qkv.dim() != 2 or qkv.stride(1) != 1:
+        raise ValueError("qkv must be a row-major [N, (Hq + 2 Hkv) * 128] tensor")
+    n = qkv.shape[0]
+    pos = positions.reshape(-1)
+    if pos.dtype != torch.int64:
+        pos = pos.to(torch.int64)
+    if pos.shape[0] != n:
+        raise ValueError(f"positions must have {n} entries")
+    pos = pos.contiguous()
+    cache = cos_sin_cache
+    if cache.dtype != torch.float32 or cache.dim() != 2 or cache.shape[1] != HEAD_DIM:
+        raise ValueError("cos_sin_cache must be fp32 [max_position, 128]")
+    cache = cache.contiguous()
+    qw = q_norm_weight.to(torch.bfloat16).contiguous()
+    kw = k_norm_weight.to(torch.bfloat16).contiguous()
+    q = torch.empty((n, num_q_heads, HEAD_DIM), dtype=torch.bfloat16, device=qkv.device)
+    k = torch.empty((n, num_kv_heads, HEAD_DIM), dtype=torch.bfloat16, device=qkv.device)
+    check(lib().qmi_qk_norm_rope(qkv.data_ptr(), qkv.stride(0), n, num_q_heads, num_kv_heads,
+                                 HEAD_DIM, qw.data_ptr(), kw.data_ptr(), pos.data_ptr(),
+                                 cache.data_ptr(), cache.shape[0], q.data_ptr(), q.stride(0),
+                                 k.data_ptr(), k.stride(0), float(eps), stream_handle(qkv.device)),
+          "qk_norm_rope")
+    return q, k
+
+
+def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
+    """``silu(gate) * up`` of a fused ``[..., 2 * inter]`` projection (one bf16 rounding)."""
+    g2 = _rows2d("gate_up", gate_up)
+    inter = g2.shape[1] // 2
+    out = torch.empty((g2.shape[0], inter), dtype=torch.bfloat16, device=g2.device)
+    check(lib().qmi_silu_mul(g2.data_ptr(), g2.stride(0), g2.shape[0], inter, out.data_ptr(),
+                             out.stride(0), stream_handle(g2.device)),
+          "silu_mul")
+    return out.view(*gate_up.shape[:-1], inter)
+
+
+# ---------------------------------------------------------------------------
 # Log-softmax gather (qwen3_grpo_train.py:46-53)
 # ---------------------------------------------------------------------------
 def _rows_view(logits: torch.Tensor, ids: torch.Tensor):

@@ -1,0 +1,673 @@
+"""Qwen3 model and continuous-batching engine on the gfx950 kernels.
+
+Keeps the call surface of qwen3-naive-inference's qwen3_naive.py so it drops
+in under its generator and GRPO loop:
+  Qwen3Config / RMSNorm / RotaryEmbedding / Qwen3Attention / Qwen3MLP /
+  Qwen3DecoderLayer / Qwen3Model / Qwen3ForCausalLM   (:109-840)
+  Qwen3Attention.forward_prefill / forward_decode    (:597-683)
+  allocate_global_kv_cache, HIP-graph decode, _prepare_step / _prepare_decode,
+  generate_continuous / generate_continuous_with_logprobs (:994-1679)
+  store_kvcache (:36) is re-exported from kernels.
+
+Inference paths (no autograd) run the HIP kernels: fused QK-RMSNorm + RoPE,
+slot-mapped KV store, paged decode / varlen prefill attention, RMSNorm /
+add+RMSNorm, SwiGLU; projections use torch GEMMs (hipBLASLt).  The batch
+``forward`` used for training keeps torch ops so autograd works, with a
+differentiable RoPE (the reference's RoPE kernel has no backward) and the
+attention core in fp32.
+"""
+from __future__ import annotations
+
+import json
+import time
+from collections import deque
+from dataclasses import dataclass
+from functools import lru_cache
+
+import numpy as np
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import kernels as K
+from .kernels import store_kvcache  # noqa: F401  (reference import surface)
+from .paged import BLOCK_SIZE, BlockManager, Sequence, build_block_tables, prepare_decode, prepare_step
+
+
+@dataclass
+class Qwen3Config:
+    hidden_size: int = 1024
+    num_attention_heads: int = 16
+    num_key_value_heads: int = 8
+    head_dim: int = 128
+    intermediate_size: int = 3072
+    num_hidden_layers: int = 28
+    vocab_size: int = 151936
+    max_position_embeddings: int = 40960
+    rms_norm_eps: float = 1e-6
+    rope_theta: float = 1000000
+    attention_bias: bool = False
+    hidden_act: str = "silu"
+    tie_word_embeddings: bool = True
+    bos_token_id: int = 151643
+    eos_token_id: int = 151645
+    dtype: str = "bfloat16"
+
+    @classmethod
+    def from_json(cls, path):
+        with open(path, "r") as f:
+            d = json.load(f)
+        return cls(
+            hidden_size=d["hidden_size"], num_attention_heads=d["num_attention_heads"],
+            num_key_value_heads=d["num_key_value_heads"],
+            head_dim=d.get("head_dim", d["hidden_size"] // d["num_attention_heads"]),
+            intermediate_size=d["intermediate_size"], num_hidden_layers=d["num_hidden_layers"],
+            vocab_size=d["vocab_size"], max_position_embeddings=d["max_position_embeddings"],
+            rms_norm_eps=d["rms_norm_eps"], rope_theta=d.get("rope_theta", 1000000),
+            attention_bias=d.get("attention_bias", False), hidden_act=d["hidden_act"],
+            tie_word_embeddings=d.get("tie_word_embeddings", True),
+            bos_token_id=d.get("bos_token_id", 151643), eos_token_id=d.get("eos_token_id", 151645))
+
+
+def _use_kernels(*tensors: torch.Tensor) -> bool:
+    """HIP kernels serve inference; autograd-tracked calls keep torch ops."""
+    if torch.is_grad_enabled() and any(t.requires_grad for t in tensors):
+        return False
+    return all(t.is_cuda for t in tensors)
+
+
+class RMSNorm(nn.Module):
+    """RMSNorm with optional fused residual add (qwen3_naive.py:150-175)."""
+
+    def __init__(self, hidden_size, eps=1e-6):
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(hidden_size))
+
+    def _torch(self, x, residual):
+        dt = x.dtype
+        xf = x.float() if residual is None else x.float() + residual.float()
+        res = None if residual is None else xf.to(dt)
+        y = (xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + self.eps)
+             * self.weight.float()).to(dt)
+        return y if residual is None else (y, res)
+
+    def forward(self, x, residual=None):
+        if x.dtype != torch.bfloat16 or not _use_kernels(x, self.weight):
+            return self._torch(x, residual)
+        if residual is None:
+            return K.rms_norm(x, self.weight, self.eps)
+        return K.add_rms_norm(x, residual, self.weight, self.eps)
+
+
+class RotaryEmbedding(nn.Module):
+    """fp32 cos/sin cache [max_position, head_dim] = cat(cos, sin) (qwen3_naive.py:380-410)."""
+
+    def __init__(self, head_dim, max_position, rope_theta):
+        super().__init__()
+        inv_freq = 1.0 / (rope_theta ** (torch.arange(0, head_dim, 2, dtype=torch.float) / head_dim))
+        pos = torch.arange(0, max_position, dtype=torch.float)
+        freqs = torch.outer(pos, inv_freq)
+        self.register_buffer("cos_sin_cache", torch.cat((freqs.cos(), freqs.sin()), dim=-1))
+
+    @staticmethod
+    def rotate(x: torch.Tensor, positions: torch.Tensor, cache: torch.Tensor) -> torch.Tensor:
+        """Differentiable half-split rotation (fp32 math, cast back)."""
+        half = x.shape[-1] // 2
+        cs = cache[positions]
+        while cs.dim() < x.dim():
+            cs = cs.unsqueeze(-2)
+        c, s = cs[..., :half], cs[..., half:]
+        x1, x2 = x[..., :half].float(), x[..., half:].float()
+        return torch.cat((x1 * c - x2 * s, x2 * c + x1 * s), dim=-1).to(x.dtype)
+
+    def forward(self, q, k, positions):
+        return (self.rotate(q, positions, self.cos_sin_cache),
+                self.rotate(k, positions, self.cos_sin_cache))
+
+
+@lru_cache(8)
+def _rope_cpu(head_dim: int, max_position: int, rope_theta: float) -> RotaryEmbedding:
+    return RotaryEmbedding(head_dim, max_position, rope_theta)
+
+
+def get_rope(head_dim: int, max_position: int, rope_theta: float) -> RotaryEmbedding:
+    """One shared cache per parameter set (the reference shares it across layers)."""
+    return _rope_cpu(head_dim, max_position, rope_theta)
+
+
+class Qwen3Attention(nn.Module):
+    """GQA attention with QK-norm and RoPE (qwen3_naive.py:413-683)."""
+
+    def __init__(self, config: Qwen3Config):
+        super().__init__()
+        self.num_heads = config.num_attention_heads
+        self.num_kv_heads = config.num_key_value_heads
+        self.head_dim = config.head_dim
+        self.hidden_size = config.hidden_size
+        self.q_size = self.num_heads * self.head_dim
+        self.kv_size = self.num_kv_heads * self.head_dim
+        self.scale = self.head_dim ** -0.5
+        self.eps = config.rms_norm_eps
+        self.qkv_proj = nn.Linear(self.hidden_size, self.q_size + 2 * self.kv_size,
+                                  bias=config.attention_bias)
+        self.o_proj = nn.Linear(self.q_size, self.hidden_size, bias=False)
+        self.q_norm = RMSNorm(self.head_dim, eps=config.rms_norm_eps)
+        self.k_norm = RMSNorm(self.head_dim, eps=config.rms_norm_eps)
+        self.k_cache = None
+        self.v_cache = None
+        # Not a registered submodule: the cache is shared between layers.
+        self.__dict__["rotary_emb"] = get_rope(self.head_dim, config.max_position_embeddings,
+                                               config.rope_theta)
+
+    def _cos_sin(self, device) -> torch.Tensor:
+        rope = self.rotary_emb
+        if rope.cos_sin_cache.device != device:
+            rope.cos_sin_cache = rope.cos_sin_cache.to(device)
+        return rope.cos_sin_cache
+
+    def _project(self, x, positions):
+        """qkv projection + fused QK-norm/RoPE kernel -> q [N,Hq,D], k [N,Hkv,D], v view."""
+        qkv = self.qkv_proj(x)
+        q, k = K.qk_norm_rope(qkv, self.q_norm.weight, self.k_norm.weight, positions,
+                              self._cos_sin(x.device), self.num_heads, self.num_kv_heads,
+                              self.eps)
+        v = qkv[:, self.q_size + self.kv_size:].view(x.shape[0], self.num_kv_heads, self.head_dim)
+        return q, k, v
+
+    # ----- batch path (training / no-cache eager forward, qwen3_naive.py:553-593) -----
+    def forward(self, x):
+        batch, seq_len, _ = x.shape
+        qkv = self.qkv_proj(x)
+        q, k, v = qkv.split([self.q_size, self.kv_size, self.kv_size], dim=-1)
+        q = self.q_norm(q.reshape(batch, seq_len, self.num_heads, self.head_dim))
+        k = self.k_norm(k.reshape(batch, seq_len, self.num_kv_heads, self.head_dim))
+        v = v.reshape(batch, seq_len, self.num_kv_heads, self.head_dim)
+        positions = torch.arange(seq_len, device=x.device)
+        cache = self._cos_sin(x.device)
+        q = RotaryEmbedding.rotate(q, positions[None, :].expand(batch, -1), cache)
+        k = RotaryEmbedding.rotate(k, positions[None, :].expand(batch, -1), cache)
+        rep = self.num_heads // self.num_kv_heads
+        # Attention core in fp32: batched bf16 products with transposed operands
+        # (and their autograd) are avoided on this platform.
+        qf = q.transpose(1, 2).float()
+        kf = k.transpose(1, 2).float().repeat_interleave(rep, dim=1)
+        vf = v.transpose(1, 2).float().repeat_interleave(rep, dim=1)
+        scores = torch.matmul(qf, kf.transpose(-2, -1).contiguous()) * self.scale
+        mask = torch.triu(torch.ones(seq_len, seq_len, device=x.device, dtype=torch.bool), 1)
+        scores = scores.masked_fill(mask, float("-inf"))
+        w = torch.softmax(scores, dim=-1)
+        o = torch.matmul(w, vf).to(x.dtype)
+        o = o.transpose(1, 2).reshape(batch, seq_len, -1)
+        return self.o_proj(o)
+
+    # ----- continuous batching (qwen3_naive.py:597-683) -----
+    def forward_prefill(self, x, positions, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
+                        max_seqlen_k, block_mapping, block_tables=None):
+        """Varlen prefill/mixed step: store the new K/V through ``block_mapping``,
+        then attend over the paged cache (prefix + earlier chunks + this chunk)."""
+        tokens = x.shape[0]
+        q, k, v = self._project(x, positions)
+        store_kvcache(k, v, self.k_cache, self.v_cache, block_mapping)
+        o = K.varlen_prefill_attention(q, self.k_cache, self.v_cache, cu_seqlens_q, cu_seqlens_k,
+                                       max_seqlen_q, max_seqlen_k, self.scale, True, block_tables)
+        return self.o_proj(o.view(tokens, -1))
+
+    def forward_decode(self, x, positions, context_lens, block_tables, slot_mapping=None):
+        """One new token per sequence: store its K/V at ``slot_mapping`` (derived
+        from the tables when None) and attend over ``context_lens + 1`` keys."""
+        batch = x.shape[0]
+        q, k, v = self._project(x, positions)
+        if slot_mapping is None:
+            ctx = context_lens.long()
+            blk = block_tables.long().gather(1, (ctx // BLOCK_SIZE)[:, None])[:, 0]
+            slot_mapping = (blk * BLOCK_SIZE + ctx % BLOCK_SIZE).to(torch.int32)
+        store_kvcache(k, v, self.k_cache, self.v_cache, slot_mapping)
+        o = K.paged_decode_attention(q, self.k_cache, self.v_cache, context_lens, block_tables,
+                                     self.scale, seqlen_bias=1)
+        return self.o_proj(o.view(batch, -1))
+
+
+class Qwen3MLP(nn.Module):
+    """SwiGLU FFN with fused gate/up (qwen3_naive.py:686-702)."""
+
+    def __init__(self, config: Qwen3Config):
+        super().__init__()
+        self.gate_up_proj = nn.Linear(config.hidden_size, 2 * config.intermediate_size, bias=False)
+        self.down_proj = nn.Linear(config.intermediate_size, config.hidden_size, bias=False)
+
+    def forward(self, x):
+        gu = self.gate_up_proj(x)
+        if gu.dtype == torch.bfloat16 and _use_kernels(gu):
+            return self.down_proj(K.silu_mul(gu))
+        gate, up = gu.chunk(2, dim=-1)
+        return self.down_proj(F.silu(gate) * up)
+
+
+class Qwen3DecoderLayer(nn.Module):
+    def __init__(self, config: Qwen3Config):
+        super().__init__()
+        self.input_layernorm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
+        self.self_attn = Qwen3Attention(config)
+        self.post_attention_layernorm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
+        self.mlp = Qwen3MLP(config)
+
+    def forward(self, x):
+        x = self.self_attn(self.input_layernorm(x)) + x
+        return self.mlp(self.post_attention_layernorm(x)) + x
+
+    def forward_prefill(self, x, positions, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
+                        max_seqlen_k, block_mapping, block_tables=None, residual=None):
+        if residual is None:
+            h, residual = self.input_layernorm(x), x
+        else:
+            h, residual = self.input_layernorm(x, residual)
+        h = self.self_attn.forward_prefill(h, positions, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
+                                           max_seqlen_k, block_mapping, block_tables)
+        h, residual = self.post_attention_layernorm(h, residual)
+        return self.mlp(h), residual
+
+    def forward_decode(self, x, positions, context_lens, block_tables, slot_mapping=None,
+                       residual=None):
+        if residual is None:
+            h, residual = self.input_layernorm(x), x
+        else:
+            h, residual = self.input_layernorm(x, residual)
+        h = self.self_attn.forward_decode(h, positions, context_lens, block_tables, slot_mapping)
+        h, residual = self.post_attention_layernorm(h, residual)
+        return self.mlp(h), residual
+
+
+class Qwen3Model(nn.Module):
+    def __init__(self, config: Qwen3Config):
+        super().__init__()
+        self.embed_tokens = nn.Embedding(config.vocab_size, config.hidden_size)
+        self.layers = nn.ModuleList([Qwen3DecoderLayer(config)
+                                     for _ in range(config.num_hidden_layers)])
+        self.norm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
+
+    def forward(self, x):
+        h = self.embed_tokens(x)
+        for layer in self.layers:
+            h = layer(h)
+        return self.norm(h)
+
+    def forward_prefill(self, x, positions, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
+                        max_seqlen_k, block_mapping, block_tables=None):
+        h = self.embed_tokens(x)
+        residual = None
+        for layer in self.layers:
+            h, residual = layer.forward_prefill(h, positions, cu_seqlens_q, cu_seqlens_k,
+                                                max_seqlen_q, max_seqlen_k, block_mapping,
+                                                block_tables, residual)
+        h, _ = self.norm(h, residual)
+        return h
+
+    def forward_decode(self, x, positions, context_lens, block_tables, slot_mapping=None):
+        h = self.embed_tokens(x)
+        residual = None
+        for layer in self.layers:
+            h, residual = layer.forward_decode(h, positions, context_lens, block_tables,
+                                               slot_mapping, residual)
+        h, _ = self.norm(h, residual)
+        return h
+
+
+# Decode batch sizes captured as HIP graphs.  The reference stops at 64 and
+# runs larger batches eagerly; the 288 GB HBM affords buckets up to 256.
+GRAPH_BATCH_SIZES = (1, 2, 4, 8, 16, 32, 48, 64, 96, 128, 160, 192, 256)
+MAX_TOKENS_PER_STEP = 2048
+
+
+class Qwen3ForCausalLM(nn.Module):
+    """Model + tied lm_head + paged-KV continuous-batching engine."""
+
+    BLOCK_SIZE = BLOCK_SIZE
+    packed_modules_mapping = {
+        "q_proj": ("qkv_proj", "q"), "k_proj": ("qkv_proj", "k"), "v_proj": ("qkv_proj", "v"),
+        "gate_proj": ("gate_up_proj", "gate"), "up_proj": ("gate_up_proj", "up"),
+    }
+
+    def __init__(self, config: Qwen3Config):
+        super().__init__()
+        self.config = config
+        self.model = Qwen3Model(config)
+        self.lm_head = nn.Linear(config.hidden_size, config.vocab_size, bias=False)
+        if config.tie_word_embeddings:
+            self.lm_head.weight = self.model.embed_tokens.weight
+        self._num_blocks = 0
+        self._graphs: dict = {}
+        self._graph_bufs = None
+        self._graph_pool = None
+        self._has_cuda_graphs = False
+
+    def forward(self, x):
+        return self.lm_head(self.model(x))
+
+    # ---------------- KV pool (qwen3_naive.py:994-1066) ----------------
+    def kv_block_bytes(self) -> int:
+        a = self.model.layers[0].self_attn
+        return 2 * len(self.model.layers) * self.BLOCK_SIZE * a.num_kv_heads * a.head_dim * 2
+
+    def _compute_num_blocks(self, gpu_memory_utilization=0.9, warmup_tokens=2048):
+        """Blocks that fit in ``utilization * total`` after weights and the peak
+        activation of a ``warmup_tokens`` forward (qwen3_naive.py:996-1035)."""
+        dev = next(self.parameters()).device
+        torch.cuda.empty_cache()
+        torch.cuda.reset_peak_memory_stats(dev)
+        with torch.no_grad():
+            ids = torch.randint(0, self.config.vocab_size, (1, warmup_tokens), device=dev)
+            _ = self.forward(ids)
+        del _
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        free, total = torch.cuda.mem_get_info(dev)
+        stats = torch.cuda.memory_stats(dev)
+        peak_act = stats["allocated_bytes.all.peak"] - stats["allocated_bytes.all.current"]
+        avail = int(total * gpu_memory_utilization - (total - free) - peak_act)
+        return max(avail // self.kv_block_bytes(), 1)
+
+    def allocate_global_kv_cache(self, num_blocks: int | None = None):
+        """One [layers, blocks, 256, Hkv, D] bf16 pool for K and one for V; each
+        layer gets its slice (qwen3_naive.py:1037-1066).  ``num_blocks`` (or a
+        preset ``_num_blocks``) skips the warm-up sizing."""
+        if num_blocks:
+            self._num_blocks = int(num_blocks)
+        if not self._num_blocks:
+            self._num_blocks = self._compute_num_blocks()
+        a0 = self.model.layers[0].self_attn
+        shape = (self._num_blocks, self.BLOCK_SIZE, a0.num_kv_heads, a0.head_dim)
+        if a0.k_cache is not None and tuple(a0.k_cache.shape) == shape:
+            return
+        dev = next(self.parameters()).device
+        n = len(self.model.layers)
+        for layer in self.model.layers:
+            layer.self_attn.k_cache = layer.self_attn.v_cache = None
+        self._graphs.clear()
+        self._has_cuda_graphs = False
+        torch.cuda.empty_cache()
+        k = torch.empty((n,) + shape, dtype=torch.bfloat16, device=dev)
+        v = torch.empty((n,) + shape, dtype=torch.bfloat16, device=dev)
+        for i, layer in enumerate(self.model.layers):
+            layer.self_attn.k_cache = k[i]
+            layer.self_attn.v_cache = v[i]
+
+    # ---------------- HIP-graph decode (qwen3_naive.py:1068-1145) ----------------
+    def _init_cuda_graphs(self, max_bs: int = GRAPH_BATCH_SIZES[-1], bt_width: int | None = None):
+        dev = next(self.parameters()).device
+        full = min(self._num_blocks, -(-self.config.max_position_embeddings // self.BLOCK_SIZE))
+        bt_width = full if bt_width is None else min(bt_width, full)
+        self._graph_bufs = {
+            "input_ids": torch.zeros(max_bs, dtype=torch.long, device=dev),
+            "positions": torch.zeros(max_bs, dtype=torch.long, device=dev),
+            "slot_mapping": torch.full((max_bs,), -1, dtype=torch.int32, device=dev),
+            "context_lens": torch.zeros(max_bs, dtype=torch.int32, device=dev),
+            "block_tables": torch.full((max_bs, bt_width), -1, dtype=torch.int32, device=dev),
+            "outputs": torch.zeros(max_bs, self.config.hidden_size, dtype=torch.bfloat16,
+                                   device=dev),
+        }
+        self._graphs = {}
+        self._graph_pool = None
+        self._has_cuda_graphs = False
+
+    def _capture_decode_graphs(self, batch_sizes=GRAPH_BATCH_SIZES):
+        """Capture forward_decode for each bucket into one shared memory pool.
+        Padded rows carry slot -1 and an empty context, so replays never write
+        stale slots.  Capture failure falls back to eager decode."""
+        bufs = self._graph_bufs
+        max_bs = bufs["input_ids"].shape[0]
+        try:
+            with torch.no_grad():
+                for bs in sorted((b for b in batch_sizes if b <= max_bs), reverse=True):
+                    args = (bufs["input_ids"][:bs], bufs["positions"][:bs],
+                            bufs["context_lens"][:bs], bufs["block_tables"][:bs],
+                            bufs["slot_mapping"][:bs])
+                    s = torch.cuda.Stream()
+                    s.wait_stream(torch.cuda.current_stream())
+                    with torch.cuda.stream(s):
+                        self.model.forward_decode(*args)
+                    torch.cuda.current_stream().wait_stream(s)
+                    graph = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(graph, pool=self._graph_pool):
+                        bufs["outputs"][:bs] = self.model.forward_decode(*args)
+                    if self._graph_pool is None:
+                        self._graph_pool = graph.pool()
+                    self._graphs[bs] = graph
+            self._has_cuda_graphs = True
+        except Exception as e:  # pragma: no cover - depends on the runtime
+            print(f"HIP graph capture failed, decoding eagerly: {e}")
+            self._graphs = {}
+            self._has_cuda_graphs = False
+
+    def _run_decode_graph(self, bs, input_ids, positions, context_lens, block_tables,
+                          slot_mapping):
+        graph_bs = next((b for b in sorted(self._graphs) if b >= bs), None)
+        bufs = self._graph_bufs
+        if graph_bs is None or block_tables.shape[1] > bufs["block_tables"].shape[1]:
+            return None
+        bufs["input_ids"][:bs] = input_ids
+        bufs["positions"][:bs] = positions
+        bufs["slot_mapping"][:bs] = slot_mapping
+        bufs["slot_mapping"][bs:graph_bs] = -1
+        bufs["context_lens"][:bs] = context_lens
+        bufs["context_lens"][bs:graph_bs] = 0
+        bufs["block_tables"][:bs, :block_tables.shape[1]] = block_tables
+        bufs["block_tables"][:bs, block_tables.shape[1]:] = -1
+        self._graphs[graph_bs].replay()
+        return bufs["outputs"][:bs]
+
+    # ---------------- step preparation (qwen3_naive.py:1147-1225) ----------------
+    def _device(self):
+        return next(self.parameters()).device
+
+    def _prepare_step(self, seqs):
+        return prepare_step(seqs, self._device(), self.BLOCK_SIZE)
+
+    def _build_block_tables(self, seqs):
+        t = torch.from_numpy(build_block_tables(seqs))
+        return t.pin_memory().to(self._device(), non_blocking=True)
+
+    def _prepare_decode(self, seqs):
+        return prepare_decode(seqs, self._device(), self.BLOCK_SIZE)
+
+    # ---------------- generation (qwen3_naive.py:1227-1679) ----------------
+    def _ensure_engine(self, graphs: bool, bt_width: int | None = None):
+        """KV pool, then decode graphs whose table width covers ``bt_width`` pages."""
+        self.allocate_global_kv_cache()
+        if not graphs:
+            return
+        have = self._graph_bufs["block_tables"].shape[1] if self._graph_bufs else 0
+        if not self._has_cuda_graphs or (bt_width is not None and have < bt_width):
+            self._init_cuda_graphs(bt_width=bt_width)
+            self._capture_decode_graphs()
+
+    def _schedule(self, waiting, running, bm):
+        """One scheduling round: decode-first walk of ``running`` with LIFO
+        preemption, then admission of ``waiting`` with chunked prefill under a
+        2048-token budget (qwen3_naive.py:1257-1341)."""
+        scheduled = []
+        budget = MAX_TOKENS_PER_STEP
+        i = 0
+        while i < len(running) and budget > 0:
+            seq = running[i]
+            if seq.kv_len >= seq.num_prompt_tokens:
+                if seq.num_completion_tokens >= seq.max_tokens:
+                    seq.status = "FINISHED"
+                    bm.deallocate(seq.block_table)
+                    seq.block_table.clear()
+                    running.pop(i)
+                    continue
+                if seq.kv_len % self.BLOCK_SIZE == 0 and not bm.free:
+                    while not bm.can_append(seq):
+                        victim = running[-1]
+                        victim.status = "WAITING"
+                        bm.deallocate(victim.block_table)
+                        victim.block_table.clear()
+                        victim.kv_len = 0
+                        victim.token_ids = victim.token_ids[:victim.num_prompt_tokens]
+                        victim.last_token = victim.token_ids[-1]
+                        victim.response_log_probs.clear()
+                        running.pop()
+                        waiting.appendleft(victim)
+                        self._preemptions += 1
+                        if victim is seq:
+                            break
+                    if seq.status == "WAITING":
+                        continue
+                bm.may_append(seq)
+                seq.num_scheduled_tokens = 1
+            else:
+                seq.num_scheduled_tokens = min(seq.num_prompt_tokens - seq.kv_len, budget)
+            scheduled.append(seq)
+            budget -= seq.num_scheduled_tokens
+            i += 1
+        while waiting and budget > 0:
+            seq = waiting[0]
+            if not seq.block_table:
+                if bm.available < seq.num_blocks:
+                    break
+                bm.allocate(seq)
+            waiting.popleft()
+            seq.status = "RUNNING"
+            running.append(seq)
+            remaining = seq.num_prompt_tokens - seq.kv_len
+            if remaining <= budget:
+                seq.num_scheduled_tokens = remaining
+            elif not scheduled:
+                seq.num_scheduled_tokens = budget
+            else:
+                waiting.appendleft(seq)
+                running.pop()
+                break
+            scheduled.append(seq)
+            budget -= seq.num_scheduled_tokens
+        return scheduled
+
+    def _sample(self, logits, temperature, top_k, want_logprobs):
+        """Temperature / top-k / softmax / multinomial (qwen3_naive.py:1413-1423) and,
+        optionally, the sampled tokens' log-probabilities (:1649-1650)."""
+        x = logits.float()
+        if temperature != 1.0:
+            x = x / temperature
+        if top_k is not None:
+            vals, idx = torch.topk(x, top_k, dim=-1)
+            x = torch.full_like(x, float("-inf")).scatter(-1, idx, vals)
+        nxt = torch.multinomial(torch.softmax(x, dim=-1), num_samples=1)
+        lp = None
+        if want_logprobs:
+            if temperature == 1.0 and top_k is None and logits.dtype == torch.bfloat16:
+                lp, _ = K.logprob_gather(logits.contiguous(), nxt[:, 0], need_lse=False)
+            else:
+                lp = torch.log_softmax(x, dim=-1).gather(-1, nxt)[:, 0]
+        return nxt[:, 0], lp
+
+    @torch.no_grad()
+    def _generate(self, prompt_ids_list, max_new_tokens, temperature, top_k, eos_token_ids,
+                  with_logprobs, use_graphs=True):
+        eos = set(eos_token_ids) if eos_token_ids is not None else None
+        prompts = [p[0].tolist() if torch.is_tensor(p) and p.dim() == 2 else
+                   (p.tolist() if torch.is_tensor(p) else list(p)) for p in prompt_ids_list]
+        # Graph table width: the pages the longest sequence of this call can need.
+        width = -(-(max(len(p) for p in prompts) + max_new_tokens + 1) // self.BLOCK_SIZE)
+        self._ensure_engine(use_graphs, bt_width=width)
+        bm = BlockManager(self._num_blocks, self.BLOCK_SIZE)
+        waiting = deque(Sequence(p, {"temperature": temperature, "max_tokens": max_new_tokens})
+                        for p in prompts)
+        all_seqs = list(waiting)
+        running: list[Sequence] = []
+        self._preemptions = 0
+        self.last_stats = {"steps": 0, "decode_steps": 0, "graph_steps": 0}
+        while waiting or running:
+            scheduled = self._schedule(waiting, running, bm)
+            if not scheduled:
+                continue
+            all_decode = all(s.num_scheduled_tokens == 1 for s in scheduled)
+            self.last_stats["steps"] += 1
+            if all_decode:
+                self.last_stats["decode_steps"] += 1
+                ids, pos, ctx, bt, slots = self._prepare_decode(scheduled)
+                h = None
+                if use_graphs and self._has_cuda_graphs:
+                    h = self._run_decode_graph(len(scheduled), ids, pos, ctx, bt, slots)
+                    if h is not None:
+                        self.last_stats["graph_steps"] += 1
+                if h is None:
+                    h = self.model.forward_decode(ids, pos, ctx, bt, slots)
+                sample_idx = None
+            else:
+                ids, pos, cu_q, cu_k, mq, mk, bmap, bt = self._prepare_step(scheduled)
+                h = self.model.forward_prefill(ids, pos, cu_q, cu_k, mq, mk, bmap, bt)
+                sample_idx, off = [], 0
+                for s in scheduled:
+                    if s.num_scheduled_tokens == 1 or s.kv_len + s.num_scheduled_tokens >= s.num_prompt_tokens:
+                        sample_idx.append(off + s.num_scheduled_tokens - 1)
+                    off += s.num_scheduled_tokens
+            for s in scheduled:
+                s.kv_len += s.num_scheduled_tokens
+                if not all_decode:
+                    bm.hash_blocks(s)
+            if sample_idx is not None and not sample_idx:
+                for s in scheduled:
+                    s.num_scheduled_tokens = 0
+                continue
+            hs = h if sample_idx is None else h[torch.tensor(sample_idx, device=h.device)]
+            nxt, lp = self._sample(self.lm_head(hs), temperature, top_k, with_logprobs)
+            toks = nxt.tolist()
+            lps = lp.tolist() if lp is not None else None
+            sampled = [s for s in scheduled if s.num_scheduled_tokens == 1 or s.kv_len >= s.num_prompt_tokens]
+            for j, s in enumerate(sampled):
+                tok = toks[j]
+                s.append_token(tok)
+                if lps is not None:
+                    s.response_log_probs.append(lps[j])
+                if (eos is not None and tok in eos) or s.num_completion_tokens >= s.max_tokens:
+                    s.status = "FINISHED"
+                    bm.deallocate(s.block_table)
+                    s.block_table.clear()
+                    running.remove(s)
+            for s in scheduled:
+                s.num_scheduled_tokens = 0
+        self.last_stats["preemptions"] = self._preemptions
+        return all_seqs
+
+    def generate_continuous(self, prompt_ids_list, max_new_tokens=256, temperature=0.6, top_k=20,
+                            eos_token_ids=None, use_graphs=True):
+        """Continuous batching with chunked prefill; returns (token ids, generated ids)."""
+        seqs = self._generate(prompt_ids_list, max_new_tokens, temperature, top_k, eos_token_ids,
+                              False, use_graphs)
+        return [s.token_ids for s in seqs], [s.token_ids[s.num_prompt_tokens:] for s in seqs]
+
+    def generate_continuous_with_logprobs(self, prompt_ids_list, max_new_tokens=256,
+                                          temperature=0.6, top_k=20, eos_token_ids=None,
+                                          use_graphs=True):
+        """As generate_continuous, also returning each sampled token's log-probability
+        under the sampling distribution and the prompt lengths."""
+        seqs = self._generate(prompt_ids_list, max_new_tokens, temperature, top_k, eos_token_ids,
+                              True, use_graphs)
+        return ([s.token_ids for s in seqs], [s.token_ids[s.num_prompt_tokens:] for s in seqs],
+                [list(s.response_log_probs) for s in seqs], [s.num_prompt_tokens for s in seqs])
+
+
+def load_weights(model: Qwen3ForCausalLM, checkpoint_path: str) -> None:
+    """Load a Qwen3 safetensors checkpoint, packing q/k/v and gate/up into the
+    fused projections (qwen3_naive.py:1682-1730); ``lm_head.weight`` is tied."""
+    from safetensors import safe_open
+    packed = model.packed_modules_mapping
+    with safe_open(checkpoint_path, framework="pt", device="cpu") as f:
+        for name in f.keys():
+            if name == "lm_head.weight":
+                continue
+            t = f.get_tensor(name)
+            for key, (fused, shard) in packed.items():
+                if key in name:
+                    p = model.get_parameter(name.replace(key, fused))
+                    if shard in ("q", "gate"):
+                        off = 0
+                    elif shard == "k":
+                        off = p.shape[0] - 2 * t.shape[0]
+                    else:
+                        off = p.shape[0] - t.shape[0]
+                    p.data[off:off + t.shape[0]] = t.to(p.device, p.dtype)
+                    break
+            else:
+                model.get_parameter(name).data.copy_(t.to(model.get_parameter(name).device))

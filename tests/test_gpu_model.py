@@ -1,0 +1,213 @@
+"""Model / engine end to end on the GPU: the kernels wired under the reference's
+call surface, checked against the CPU oracle forward (fp32) and for the
+chunked / prefix-cache / decode self-consistency the reference's own tests
+assert (top-1 equal, top-20 overlap)."""
+import pytest
+import torch
+
+from oracle import model as OM
+
+pytestmark = pytest.mark.gpu
+
+LAYERS, VOCAB = 2, 2048
+
+
+@pytest.fixture(scope="module")
+def model(pkg, gpu):
+    cfg = pkg.Qwen3Config(num_hidden_layers=LAYERS, vocab_size=VOCAB)
+    torch.manual_seed(0)
+    m = pkg.Qwen3ForCausalLM(cfg)
+    with torch.no_grad():
+        for name, p in m.named_parameters():
+            if "norm" in name:
+                p.uniform_(0.8, 1.2)
+            elif "embed" in name:
+                p.normal_(0, 0.25)              # tied lm_head: logits O(5)
+            elif p.dim() == 2:
+                p.normal_(0, 0.02)
+    m = m.to(gpu).to(torch.bfloat16).eval()
+    m.allocate_global_kv_cache(num_blocks=64)
+    return m
+
+
+def _oracle_logits(model, ids):
+    return OM.qwen3_logits(model.state_dict(), torch.as_tensor(ids)[None], LAYERS)[0]
+
+
+def _prefill(pkg, model, seq, n):
+    seq.num_scheduled_tokens = n
+    ids, pos, cu_q, cu_k, mq, mk, bmap, bt = model._prepare_step([seq])
+    with torch.no_grad():
+        h = model.model.forward_prefill(ids, pos, cu_q, cu_k, mq, mk, bmap, bt)
+        logits = model.lm_head(h).float()
+    seq.kv_len += n
+    seq.num_scheduled_tokens = 0
+    return logits
+
+
+def _rel(a, b):
+    a, b = a.float().cpu(), b.float().cpu()
+    return ((a - b).norm() / b.norm()).item()
+
+
+def _topk_overlap(a, b, k=20):
+    return len(set(torch.topk(a.float().cpu(), k).indices.tolist())
+               & set(torch.topk(b.float().cpu(), k).indices.tolist()))
+
+
+def test_prefill_logits_match_oracle(pkg, model):
+    g = torch.Generator().manual_seed(1)
+    toks = torch.randint(0, VOCAB, (300,), generator=g).tolist()
+    bm = pkg.BlockManager(64)
+    s = pkg.Sequence(toks)
+    bm.allocate(s)
+    print("[model] prefill vs oracle", flush=True)
+    logits = _prefill(pkg, model, s, len(toks))
+    ref = _oracle_logits(model, toks)
+    assert _rel(logits, ref) < 3e-2
+    assert (logits.argmax(-1).cpu() == ref.argmax(-1)).float().mean() > 0.9
+
+
+def test_chunked_vs_unchunked_prefill(pkg, model):
+    """The reference's chunked-prefill check: last-token logits of a ~500-token
+    prompt prefilled whole vs in 256-token chunks: top-1 equal, top-20 >= 19."""
+    g = torch.Generator().manual_seed(2)
+    toks = torch.randint(0, VOCAB, (517,), generator=g).tolist()
+    bm = pkg.BlockManager(64)
+    a = pkg.Sequence(toks)
+    bm.allocate(a)
+    print("[model] chunked vs unchunked", flush=True)
+    full = _prefill(pkg, model, a, len(toks))[-1]
+    bm2 = pkg.BlockManager(64)
+    b = pkg.Sequence(toks)
+    bm2.allocate(b)
+    while b.kv_len < len(toks):
+        last = _prefill(pkg, model, b, min(256, len(toks) - b.kv_len))[-1]
+        bm2.hash_blocks(b)
+    assert last.argmax().item() == full.argmax().item()
+    assert _topk_overlap(last, full) >= 19
+    assert _rel(last, full) < 1e-2
+
+
+def test_prefix_cached_prefill_matches_full_forward(pkg, model):
+    """The reference's prefix-cache check: a prompt whose first 512 tokens hit
+    the prefix cache, prefilled from kv_len=512, against the full forward."""
+    g = torch.Generator().manual_seed(3)
+    prefix = torch.randint(0, VOCAB, (512,), generator=g).tolist()
+    bm = pkg.BlockManager(64)
+    a = pkg.Sequence(prefix + [5, 6, 7])
+    bm.allocate(a)
+    _prefill(pkg, model, a, a.num_prompt_tokens)
+    a.num_scheduled_tokens = a.num_prompt_tokens
+    bm.hash_blocks(a)
+    a.num_scheduled_tokens = 0
+    toks = prefix + torch.randint(0, VOCAB, (40,), generator=g).tolist()
+    b = pkg.Sequence(toks)
+    bm.allocate(b)
+    assert b.kv_len == 512 and b.block_table[:2] == a.block_table[:2]
+    print("[model] prefix cached", flush=True)
+    logits = _prefill(pkg, model, b, len(toks) - 512)
+    ref = _oracle_logits(model, toks)[512:]
+    assert logits[-1].argmax().item() == ref[-1].argmax().item()
+    assert _topk_overlap(logits[-1], ref[-1]) >= 15
+    assert _rel(logits, ref) < 3e-2
+
+
+def test_teacher_forced_decode_matches_oracle_and_graph(pkg, model):
+    g = torch.Generator().manual_seed(4)
+    toks = torch.randint(0, VOCAB, (254,), generator=g).tolist()
+    extra = torch.randint(0, VOCAB, (6,), generator=g).tolist()
+    bm = pkg.BlockManager(64)
+    s = pkg.Sequence(toks)
+    bm.allocate(s)
+    _prefill(pkg, model, s, len(toks))
+    outs = []
+    print("[model] teacher-forced decode", flush=True)
+    for t in extra:                               # crosses the 256 page boundary
+        s.append_token(t)
+        bm.may_append(s)
+        ids, pos, ctx, bt, slot = model._prepare_decode([s])
+        with torch.no_grad():
+            h = model.model.forward_decode(ids, pos, ctx, bt, slot)
+            outs.append(model.lm_head(h)[0].float())
+        s.kv_len += 1
+    ref = _oracle_logits(model, toks + extra)[len(toks):]
+    got = torch.stack(outs)
+    assert _rel(got, ref) < 3e-2
+    assert (got.argmax(-1).cpu() == ref.argmax(-1)).all()
+
+
+def test_graph_decode_equals_eager(pkg, model):
+    g = torch.Generator().manual_seed(5)
+    bm = pkg.BlockManager(64)
+    seqs = []
+    for n in (100, 257, 31):
+        s = pkg.Sequence(torch.randint(0, VOCAB, (n,), generator=g).tolist())
+        bm.allocate(s)
+        _prefill(pkg, model, s, n)
+        s.append_token(7)
+        bm.may_append(s)
+        seqs.append(s)
+    ids, pos, ctx, bt, slot = model._prepare_decode(seqs)
+    print("[model] graph vs eager decode", flush=True)
+    with torch.no_grad():
+        eager = model.model.forward_decode(ids, pos, ctx, bt, slot).clone()
+        model._init_cuda_graphs(max_bs=8, bt_width=4)
+        model._capture_decode_graphs(batch_sizes=(4, 8))
+        assert model._has_cuda_graphs
+        first = None
+        for _ in range(3):
+            out = model._run_decode_graph(3, ids, pos, ctx, bt, slot).clone()
+            torch.cuda.synchronize()
+            first = out if first is None else first
+            assert torch.equal(out, first)          # replays are deterministic
+        # The graph runs the GEMMs at the padded batch (4 rows), eager at 3 rows:
+        # hipBLASLt may pick different kernels, so compare within bf16 tolerance.
+        assert (first.float() - eager.float()).abs().max().item() < 5e-2
+    model._has_cuda_graphs = False
+    model._graphs = {}
+
+
+def test_generate_continuous_and_logprobs(pkg, model):
+    g = torch.Generator().manual_seed(6)
+    prompts = [torch.randint(0, VOCAB, (1, n), generator=g) for n in (20, 300, 77)]
+    print("[model] generate_continuous", flush=True)
+    torch.manual_seed(0)
+    seq_tokens, gen = model.generate_continuous(prompts, max_new_tokens=12, temperature=1.0,
+                                                top_k=None)
+    assert [len(x) for x in gen] == [12, 12, 12]
+    assert model.last_stats["graph_steps"] > 0
+    torch.manual_seed(0)
+    toks, gen2, lps, plens = model.generate_continuous_with_logprobs(
+        prompts, max_new_tokens=12, temperature=1.0, top_k=None)
+    assert plens == [20, 300, 77] and [len(x) for x in lps] == [12, 12, 12]
+    # Old log-probs equal the log-softmax of the model's own logits at the
+    # previous position (teacher-forced recomputation through prefill).
+    bm = pkg.BlockManager(64)
+    for b in range(3):
+        s = pkg.Sequence(toks[b][:-1])
+        bm.allocate(s)
+        logits = _prefill(pkg, model, s, len(toks[b]) - 1)
+        lp = torch.log_softmax(logits, -1)
+        tgt = torch.tensor(toks[b][plens[b]:], device=lp.device)
+        re = lp[plens[b] - 1:].gather(-1, tgt[:, None])[:, 0].cpu()
+        d = (re - torch.tensor(lps[b])).abs()
+        assert d.max().item() < 0.25 and d.median().item() < 0.05
+        bm.deallocate(s.block_table)
+
+
+def test_generation_with_preemption(pkg, model):
+    """A pool too small for every sequence at once forces LIFO preemption; all
+    sequences still finish with the requested number of tokens."""
+    model.allocate_global_kv_cache(num_blocks=6)
+    try:
+        g = torch.Generator().manual_seed(7)
+        prompts = [torch.randint(0, VOCAB, (1, 250), generator=g) for _ in range(4)]
+        print("[model] preemption", flush=True)
+        _, gen = model.generate_continuous(prompts, max_new_tokens=20, temperature=1.0,
+                                           top_k=20, use_graphs=False)
+        assert [len(x) for x in gen] == [20] * 4
+        assert model.last_stats["preemptions"] > 0
+    finally:
+        model._num_blocks = 0
+        model.allocate_global_kv_cache(num_blocks=64)

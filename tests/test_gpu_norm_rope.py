@@ -1,0 +1,79 @@
+"""RMSNorm / add+RMSNorm / fused QK-norm+RoPE / SwiGLU kernels against the
+oracle.  Outputs are bf16; the tolerance is one bf16 ulp of the value (the
+kernels compute in fp32 with a different summation order)."""
+import pytest
+import torch
+
+from oracle import norm_rope as NR
+
+pytestmark = pytest.mark.gpu
+
+
+def ulp_close(a, b, ulps=1.0):
+    a = a.float().cpu()
+    b = b.float().cpu()
+    tol = ulps * 2.0 ** -7 * b.abs().clamp_min(2.0 ** -100) + 1e-30
+    bad = ((a - b).abs() > tol).sum().item()
+    return bad == 0, bad, (a - b).abs().max().item()
+
+
+@pytest.mark.parametrize("n", [128, 1024, 3072])
+def test_rms_norm(pkg, gpu, n):
+    g = torch.Generator().manual_seed(n)
+    x = (torch.randn(37, n, generator=g) * 3).to(torch.bfloat16)
+    w = (torch.rand(n, generator=g) + 0.5).to(torch.bfloat16)
+    print(f"[norm] rms n={n}", flush=True)
+    y = pkg.kernels.rms_norm(x.to(gpu), w.to(gpu), 1e-6)
+    torch.cuda.synchronize()
+    ok, bad, mx = ulp_close(y, NR.rms_norm(x, w, 1e-6))
+    assert ok, f"{bad} elements beyond 1 ulp (max diff {mx})"
+
+
+def test_add_rms_norm(pkg, gpu):
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(64, 1024, generator=g).to(torch.bfloat16)
+    r = torch.randn(64, 1024, generator=g).to(torch.bfloat16)
+    w = (torch.rand(1024, generator=g) + 0.5).to(torch.bfloat16)
+    print("[norm] add+rms", flush=True)
+    y, res = pkg.kernels.add_rms_norm(x.to(gpu), r.to(gpu), w.to(gpu), 1e-6)
+    torch.cuda.synchronize()
+    ry, rres = NR.add_rms_norm(x, r, w, 1e-6)
+    assert torch.equal(res.cpu(), rres)          # bf16(x + r): exact
+    ok, bad, mx = ulp_close(y, ry)
+    assert ok, f"{bad} elements beyond 1 ulp (max diff {mx})"
+
+
+def test_qk_norm_rope(pkg, gpu):
+    g = torch.Generator().manual_seed(2)
+    n, hq, hkv = 50, 16, 8
+    qkv = (torch.randn(n, (hq + 2 * hkv) * 128, generator=g) * 2).to(torch.bfloat16)
+    qw = (torch.rand(128, generator=g) + 0.5).to(torch.bfloat16)
+    kw = (torch.rand(128, generator=g) + 0.5).to(torch.bfloat16)
+    pos = torch.randint(0, 40960, (n,), generator=g)
+    pos[0] = 0
+    cache = NR.rope_cache(128, 40960, 1e6)
+    print("[norm] qk norm + rope", flush=True)
+    q, k = pkg.kernels.qk_norm_rope(qkv.to(gpu), qw.to(gpu), kw.to(gpu), pos.to(gpu),
+                                    cache.to(gpu), hq, hkv, 1e-6)
+    torch.cuda.synchronize()
+    qn = NR.rms_norm(qkv[:, :hq * 128].view(n, hq, 128), qw, 1e-6)
+    kn = NR.rms_norm(qkv[:, hq * 128:(hq + hkv) * 128].view(n, hkv, 128), kw, 1e-6)
+    rq = NR.apply_rope(qn, pos, cache, torch.bfloat16)
+    rk = NR.apply_rope(kn, pos, cache, torch.bfloat16)
+    # Two roundings in the chain (norm output, rope output): allow 2 ulps.
+    for got, ref in ((q, rq), (k, rk)):
+        ok, bad, mx = ulp_close(got, ref, 2.0)
+        assert ok, f"{bad} elements beyond 2 ulp (max diff {mx})"
+    assert torch.equal(q[0].cpu(), qn[0])        # position 0 rotates by identity
+
+
+def test_silu_mul(pkg, gpu):
+    g = torch.Generator().manual_seed(3)
+    gu = (torch.randn(33, 2 * 3072, generator=g) * 2).to(torch.bfloat16)
+    print("[norm] silu*mul", flush=True)
+    out = pkg.kernels.silu_mul(gu.to(gpu))
+    torch.cuda.synchronize()
+    gf, uf = gu[:, :3072].float(), gu[:, 3072:].float()
+    ref = (torch.nn.functional.silu(gf) * uf).to(torch.bfloat16)
+    ok, bad, mx = ulp_close(out, ref, 1.0)
+    assert ok, f"{bad} elements beyond 1 ulp (max diff {mx})"

@@ -1,0 +1,218 @@
+"""Host-side paged-KV logic (CPU): BlockManager, step preparation and the
+scheduler's LIFO preemption.  Expected values are hand-derived from the
+reference's rules (qwen3_naive.py:240-375, :1147-1225, :1257-1341)."""
+import importlib
+from collections import deque
+
+import numpy as np
+import pytest
+import torch
+from hypothesis import given, settings
+from hypothesis import strategies as st
+
+from oracle import paged as OP
+
+pkg = importlib.import_module("qwen3-naive-inference_amd")
+paged = pkg.paged
+BM, Seq = paged.BlockManager, paged.Sequence
+
+
+def test_hash_matches_oracle_and_known_answer():
+    assert BM.compute_hash([1, 2]) == 35
+    rng = np.random.default_rng(0)
+    for _ in range(20):
+        toks = rng.integers(0, 151936, size=int(rng.integers(1, 300))).tolist()
+        pre = int(rng.integers(0, 2**63))
+        assert BM.compute_hash(toks, pre) == OP.compute_hash_u64(toks, pre)
+
+
+def _prefilled(bm, tokens):
+    s = Seq(tokens)
+    bm.allocate(s)
+    s.num_scheduled_tokens = s.num_prompt_tokens - s.kv_len
+    s.kv_len = s.num_prompt_tokens
+    bm.hash_blocks(s)
+    s.num_scheduled_tokens = 0
+    return s
+
+
+def test_allocate_pops_from_end_of_free_list():
+    bm = BM(10)
+    s = Seq(list(range(600)))  # 3 pages
+    bm.allocate(s)
+    assert s.block_table == [9, 8, 7] and s.kv_len == 0
+    assert bm.available == 7 and [bm.ref_count[b] for b in (9, 8, 7)] == [1, 1, 1]
+
+
+def test_prefix_sharing_and_refcounts():
+    bm = BM(16)
+    prefix = list(range(1000, 1512))          # two full pages
+    a = _prefilled(bm, prefix + [1, 2, 3])
+    b = Seq(prefix + [7, 8, 9, 10])
+    bm.allocate(b)
+    assert b.block_table[:2] == a.block_table[:2]
+    assert b.kv_len == 512                    # prefix hit sets kv_len
+    assert all(bm.ref_count[x] == 2 for x in a.block_table[:2])
+    assert b.block_table[2] not in a.block_table
+
+
+def test_full_prompt_never_shares_last_page():
+    bm = BM(8)
+    toks = list(range(512))                   # exactly 2 pages
+    _prefilled(bm, toks)
+    c = Seq(toks)
+    bm.allocate(c)
+    assert c.kv_len == 256                    # loop stops at num_blocks - 1
+
+
+def test_freed_hashed_pages_are_revived():
+    bm = BM(8)
+    toks = list(range(300, 812)) + [5]
+    a = _prefilled(bm, toks)
+    shared = a.block_table[:2]
+    bm.deallocate(a.block_table)
+    assert all(b in bm.free for b in a.block_table)
+    c = Seq(toks)
+    bm.allocate(c)
+    assert c.block_table[:2] == shared and c.kv_len == 512
+    assert all(b not in bm.free and bm.ref_count[b] == 1 for b in shared)
+
+
+def test_reallocated_page_loses_its_hash():
+    bm = BM(3)
+    a = _prefilled(bm, list(range(256)) + [1])   # pages 2 (hashed), 1
+    h = bm.block_hash[a.block_table[0]]
+    bm.deallocate(a.block_table)                # free = [0, 2, 1]
+    d = Seq(list(range(900, 1400)))             # 2 pages: pops 1 then 2
+    bm.allocate(d)
+    assert h not in bm.hash_to_block and bm.block_hash[2] == -1
+
+
+def test_hash_collision_guard(monkeypatch):
+    bm = BM(8)
+    monkeypatch.setattr(BM, "compute_hash", staticmethod(lambda toks, prefix=-1: 42))
+    _prefilled(bm, list(range(256)) + [0])
+    b = Seq(list(range(1000, 1256)) + [0])      # same (forced) hash, different tokens
+    bm.allocate(b)
+    assert b.kv_len == 0
+
+
+@settings(max_examples=60, deadline=None)
+@given(st.lists(st.tuples(st.integers(0, 3), st.integers(1, 700), st.integers(0, 2)),
+                min_size=1, max_size=25))
+def test_blockmanager_invariants(ops):
+    """Refcount conservation, free/used partition and hash-table consistency
+    under random allocate / decode-append / free sequences."""
+    bm = BM(24)
+    live = []
+    prefixes = [list(range(i * 1000, i * 1000 + 512)) for i in range(3)]
+    for kind, n, p in ops:
+        if kind <= 1:
+            toks = prefixes[p][: min(n, 512)] + list(range(5000, 5000 + max(0, n - 512)))
+            s = Seq(toks)
+            if bm.available < s.num_blocks:
+                continue
+            bm.allocate(s)
+            s.num_scheduled_tokens = s.num_prompt_tokens - s.kv_len
+            s.kv_len = s.num_prompt_tokens
+            bm.hash_blocks(s)
+            live.append(s)
+        elif kind == 2 and live:
+            s = live[n % len(live)]
+            if bm.can_append(s):
+                bm.may_append(s)
+                s.append_token(n)
+                s.kv_len += 1
+        elif live:
+            s = live.pop(n % len(live))
+            bm.deallocate(s.block_table)
+        used = {}
+        for s in live:
+            for b in s.block_table:
+                used[b] = used.get(b, 0) + 1
+        assert all(bm.ref_count[b] == c for b, c in used.items())
+        assert set(bm.free) == set(range(24)) - set(used)
+        assert len(bm.free) == len(set(bm.free))
+        assert all(bm.ref_count[b] == 0 for b in bm.free)
+        for h, b in bm.hash_to_block.items():
+            assert bm.block_hash[b] == h
+
+
+def test_prepare_step_chunked_kv_tracking():
+    """Mirror of the reference's kv_len tracking case: each chunk gives
+    cu_q[-1] == scheduled and cu_k[-1] == kv_before + scheduled."""
+    bm = BM(16)
+    s = Seq(list(range(1500)))
+    bm.allocate(s)
+    hist = []
+    while s.kv_len < s.num_prompt_tokens:
+        s.num_scheduled_tokens = min(512, s.num_prompt_tokens - s.kv_len)
+        before = s.kv_len
+        ids, pos, cu_q, cu_k, mq, mk, bmap, bt = paged.prepare_step([s])
+        assert cu_q[-1].item() == s.num_scheduled_tokens
+        assert cu_k[-1].item() == before + s.num_scheduled_tokens
+        assert pos.tolist() == list(range(before, before + s.num_scheduled_tokens))
+        assert bmap.tolist() == OP.token_slots(s.block_table, before, before + s.num_scheduled_tokens)
+        s.kv_len += s.num_scheduled_tokens
+        bm.hash_blocks(s)
+        hist.append((before, s.kv_len, s.num_scheduled_tokens))
+        s.num_scheduled_tokens = 0
+    assert s.kv_len == 1500
+    assert all(a < b and b - a == n for a, b, n in hist)
+
+
+def test_prepare_step_mixed_batch():
+    """Mirror of the reference's mixed-batch case: two decodes + a 512 chunk."""
+    bm = BM(16)
+    s1, s2 = Seq(list(range(7))), Seq(list(range(11)))
+    for s in (s1, s2):
+        bm.allocate(s)
+        s.kv_len = s.num_prompt_tokens
+        s.append_token(99)
+        s.num_scheduled_tokens = 1
+    long = Seq(list(range(1200)))
+    bm.allocate(long)
+    long.num_scheduled_tokens = 512
+    ids, pos, cu_q, cu_k, mq, mk, bmap, bt = paged.prepare_step([s1, s2, long])
+    assert cu_q.tolist() == [0, 1, 2, 514]
+    assert cu_k.tolist() == [0, 8, 20, 532]
+    assert tuple(bt.shape) == (3, 5) and mq == 512 and mk == 512
+    assert ids[:2].tolist() == [99, 99] and pos[:2].tolist() == [7, 11]
+    assert bmap[:2].tolist() == [s1.block_table[0] * 256 + 7, s2.block_table[0] * 256 + 11]
+    assert bt[0].tolist() == [s1.block_table[0], -1, -1, -1, -1]
+
+
+def test_prepare_decode_slots():
+    bm = BM(8)
+    s = Seq(list(range(255)))
+    bm.allocate(s)
+    s.kv_len = 255
+    s.append_token(3)            # 256 tokens; next K/V goes to position 255
+    ids, pos, ctx, bt, slot = paged.prepare_decode([s])
+    assert slot.tolist() == [s.block_table[0] * 256 + 255]
+    assert ctx.tolist() == [255] and pos.tolist() == [255] and ids.tolist() == [3]
+
+
+def test_scheduler_lifo_preemption():
+    """At a page boundary with no free page, the newest running sequence is
+    preempted: its pages are freed, it restarts from its prompt and goes to
+    the front of the waiting queue (qwen3_naive.py:1280-1301)."""
+    cfg = pkg.Qwen3Config(num_hidden_layers=1, vocab_size=64, max_position_embeddings=4096)
+    eng = pkg.Qwen3ForCausalLM(cfg)
+    eng._preemptions = 0
+    bm = BM(3)
+    a, b = Seq(list(range(256))), Seq(list(range(300, 556)))
+    running = []
+    for s in (a, b):
+        bm.allocate(s)               # one page each
+        s.kv_len = 256               # prompt done, next write opens a new page
+        s.append_token(1)
+        s.status = "RUNNING"
+        running.append(s)
+    waiting = deque()
+    bm.allocate(Seq(list(range(10))))  # consume the last free page
+    sched = eng._schedule(waiting, running, bm)
+    assert sched == [a] and running == [a]
+    assert list(waiting) == [b] and b.status == "WAITING"
+    assert b.kv_len == 0 and b.token_ids == list(range(300, 556)) and not b.block_table
+    assert len(a.block_table) == 2 and eng._preemptions == 1
