@@ -169,6 +169,214 @@ def leg_prefill(torch, pkg, W, dev, steps, warmup):
                 q_tokens=sum(int(c["cu_seqlens_q"][-1]) for c in calls))
 
 
+# ---------------------------------------------------------------------------
+# End-to-end GRPO rollout + loss (config 5) and the reference-path baseline.
+class ReferencePath:
+    """Runs the engine the way the reference's non-kernel path would on this
+    GPU: torch ops for RMSNorm / RoPE / SwiGLU / KV store, attention as torch
+    SDPA over K/V gathered through the block table (flash-attn is not in this
+    image), eager decode without graphs.  Bench-only: the product has one
+    backend."""
+
+    def __init__(self, torch, pkg):
+        self.torch, self.pkg = torch, pkg
+        self.QN = pkg.qwen3_naive
+
+    def _project(self, attn, x, positions):
+        t = self.torch
+        qkv = attn.qkv_proj(x)
+        n = x.shape[0]
+        q, k, v = qkv.split([attn.q_size, attn.kv_size, attn.kv_size], dim=-1)
+        q = attn.q_norm(q.reshape(n, attn.num_heads, attn.head_dim))
+        k = attn.k_norm(k.reshape(n, attn.num_kv_heads, attn.head_dim))
+        cache = attn._cos_sin(x.device)
+        rot = self.QN.RotaryEmbedding.rotate
+        return rot(q, positions, cache), rot(k, positions, cache), v.reshape(n, attn.num_kv_heads, attn.head_dim)
+
+    def _store(self, attn, k, v, slots):
+        # Eager steps carry no -1 (padding) slots, so a plain index_copy_ is exact.
+        row = attn.num_kv_heads * attn.head_dim
+        idx = slots.long()
+        attn.k_cache.view(-1, row).index_copy_(0, idx, k.reshape(-1, row))
+        attn.v_cache.view(-1, row).index_copy_(0, idx, v.reshape(-1, row))
+
+    attention_kind = "torch SDPA (memory-efficient backend, bf16)"
+
+    def _sdpa(self, q, k, v, mask):
+        t = self.torch
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+        if ReferencePath.attention_kind.startswith("torch SDPA"):
+            try:
+                with sdpa_kernel([SDPBackend.EFFICIENT_ATTENTION, SDPBackend.FLASH_ATTENTION]):
+                    return t.nn.functional.scaled_dot_product_attention(q, k, v, attn_mask=mask)
+            except RuntimeError:
+                ReferencePath.attention_kind = "fp32 matmul attention (no fused SDPA kernel)"
+        # fp32 products: batched bf16 products with transposed operands are
+        # avoided on this platform.
+        s = t.matmul(q.float(), k.float().transpose(-2, -1).contiguous()) * q.shape[-1] ** -0.5
+        s = s.masked_fill(~mask, float("-inf"))
+        return t.matmul(t.softmax(s, -1), v.float()).to(q.dtype)
+
+    def decode(self, attn, x, positions, context_lens, block_tables, slot_mapping=None):
+        t = self.torch
+        q, k, v = self._project(attn, x, positions)
+        self._store(attn, k, v, slot_mapping)
+        bsz, w = block_tables.shape
+        bt = block_tables.clamp(min=0).long()
+        kk = attn.k_cache[bt].reshape(bsz, w * 256, attn.num_kv_heads, attn.head_dim)
+        vv = attn.v_cache[bt].reshape(bsz, w * 256, attn.num_kv_heads, attn.head_dim)
+        rep = attn.num_heads // attn.num_kv_heads
+        kk = kk.transpose(1, 2).repeat_interleave(rep, 1)
+        vv = vv.transpose(1, 2).repeat_interleave(rep, 1)
+        mask = (t.arange(w * 256, device=x.device)[None, :] <= context_lens.long()[:, None])
+        o = self._sdpa(q[:, :, None, :], kk, vv, mask[:, None, None, :])
+        return attn.o_proj(o.reshape(bsz, -1))
+
+    def prefill(self, attn, x, positions, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+                block_mapping, block_tables=None):
+        t = self.torch
+        q, k, v = self._project(attn, x, positions)
+        self._store(attn, k, v, block_mapping)
+        cq, ck = cu_seqlens_q.tolist(), cu_seqlens_k.tolist()
+        rep = attn.num_heads // attn.num_kv_heads
+        outs = []
+        for b in range(len(cq) - 1):
+            lq, lk = cq[b + 1] - cq[b], ck[b + 1] - ck[b]
+            if lq == 0:
+                continue
+            pos = t.arange(lk, device=x.device)
+            blk = block_tables[b].long()[pos // 256]
+            kk = attn.k_cache[blk, pos % 256].transpose(0, 1).repeat_interleave(rep, 0)
+            vv = attn.v_cache[blk, pos % 256].transpose(0, 1).repeat_interleave(rep, 0)
+            i = t.arange(lq, device=x.device)[:, None]
+            mask = pos[None, :] <= i + (lk - lq)
+            qb = q[cq[b]:cq[b + 1]].transpose(0, 1)
+            outs.append(self._sdpa(qb[None], kk[None], vv[None], mask[None, None])[0].transpose(0, 1))
+        o = t.cat(outs).reshape(x.shape[0], -1)
+        return attn.o_proj(o)
+
+    def __enter__(self):
+        QN, me = self.QN, self
+        self._saved = (QN._use_kernels, QN.Qwen3Attention.forward_decode,
+                       QN.Qwen3Attention.forward_prefill)
+        QN._use_kernels = lambda *a: False
+        QN.Qwen3Attention.forward_decode = lambda attn, *a, **k: me.decode(attn, *a, **k)
+        QN.Qwen3Attention.forward_prefill = lambda attn, *a, **k: me.prefill(attn, *a, **k)
+        return self
+
+    def __exit__(self, *exc):
+        QN = self.QN
+        QN._use_kernels, QN.Qwen3Attention.forward_decode, QN.Qwen3Attention.forward_prefill = self._saved
+        return False
+
+
+def make_rollout_model(torch, pkg, dev, pool_gb=40.0):
+    """Random-init Qwen3-0.6B (28 layers, tied lm_head) in bf16 with a KV pool of
+    ``pool_gb`` GB (40 GB -> 1,362 blocks of 29.36 MB)."""
+    torch.manual_seed(0)
+    cfg = pkg.Qwen3Config()
+    with torch.device(dev):
+        model = pkg.Qwen3ForCausalLM(cfg)
+    model = model.to(torch.bfloat16).eval()
+    model.allocate_global_kv_cache(num_blocks=int(pool_gb * 1e9 // model.kv_block_bytes()))
+    return model
+
+
+def rollout_prompts(torch, n_prompts=32, group=8, prompt_len=128, vocab=151936, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    base = [torch.randint(0, vocab, (1, prompt_len), generator=g) for _ in range(n_prompts)]
+    return [p for p in base for _ in range(group)]
+
+
+def grpo_loss_after_rollout(torch, pkg, model, seqs, plens, lps, n_prompts, group, micro=16, seed=0):
+    """New log-probs of every generated token (prefill forward, micro-batched),
+    seeded Bernoulli(0.5) rewards, group advantages and the clipped loss
+    (per-sequence masked mean), next-token alignment."""
+    dev = next(model.parameters()).device
+    g = torch.Generator().manual_seed(seed)
+    rewards = torch.bernoulli(torch.full((len(seqs),), 0.5), generator=g).to(dev)
+    pids = torch.arange(n_prompts).repeat_interleave(group).to(dev)
+    total, n_seq = 0.0, len(seqs)
+    with torch.no_grad():
+        for s0 in range(0, n_seq, micro):
+            chunk = seqs[s0:s0 + micro]
+            T = max(len(x) for x in chunk)
+            bm = pkg.BlockManager(model._num_blocks)
+            objs = []
+            for toks in chunk:
+                sq = pkg.Sequence(toks)
+                bm.allocate(sq)
+                sq.kv_len = 0
+                sq.num_scheduled_tokens = len(toks)
+                objs.append(sq)
+            ids, pos, cu_q, cu_k, mq, mk, bmap, bt = model._prepare_step(objs)
+            h = model.model.forward_prefill(ids, pos, cu_q, cu_k, mq, mk, bmap, bt)
+            logits = model.lm_head(h).view(len(chunk), T, -1)
+            ids2 = ids.view(len(chunk), T)
+            old = torch.zeros((len(chunk), T), dtype=torch.float32, device=dev)
+            mask = torch.zeros_like(old)
+            for i, (pl, lp) in enumerate(zip(plens[s0:s0 + micro], lps[s0:s0 + micro])):
+                old[i, pl:pl + len(lp)] = torch.tensor(lp, device=dev)
+                mask[i, pl:pl + len(lp)] = 1.0
+            loss, _, _ = pkg.grpo_fused_loss(logits, ids2, old, mask, rewards[s0:s0 + micro],
+                                             pids[s0:s0 + micro], 1e-4, 0.2, "seq", shift=True)
+            total += loss.item() * len(chunk) / n_seq
+            del logits, h
+    return total
+
+
+def leg_rollout(torch, pkg, dev, new_tokens=1024, compare_tokens=64):
+    """Config 5: 32 prompts x group 8 = 256 sequences, 128-token prompts, T=1.0,
+    no top-k, ``new_tokens`` generated tokens each, continuous batching with the
+    2048-token step budget and LIFO preemption, ~40 GB pool; then the GRPO
+    loss over the generated tokens.  Also times ours and the reference path at
+    ``compare_tokens`` new tokens on the same workload."""
+    model = make_rollout_model(torch, pkg, dev)
+    prompts = rollout_prompts(torch)
+    n_tok = len(prompts)
+    log("rollout: warm-up / graph capture")
+    model.generate_continuous_with_logprobs(prompts[:16], max_new_tokens=4, temperature=1.0,
+                                            top_k=None)
+    out = {}
+    # Short comparison against the reference path (same scheduler, torch attention).
+    for name in ("ours_short", "reference_path_short"):
+        torch.manual_seed(1)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        if name == "ours_short":
+            model.generate_continuous_with_logprobs(prompts, max_new_tokens=compare_tokens,
+                                                    temperature=1.0, top_k=None)
+        else:
+            with ReferencePath(torch, pkg):
+                model.generate_continuous_with_logprobs(prompts, max_new_tokens=compare_tokens,
+                                                        temperature=1.0, top_k=None,
+                                                        use_graphs=False)
+        torch.cuda.synchronize()
+        out[name] = n_tok * compare_tokens / (time.perf_counter() - t0)
+        log(f"rollout: {name} {out[name]:.0f} tok/s")
+    log(f"rollout: full run ({n_tok} x {new_tokens} tokens)")
+    torch.manual_seed(2)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    toks, gen, lps, plens = model.generate_continuous_with_logprobs(
+        prompts, max_new_tokens=new_tokens, temperature=1.0, top_k=None)
+    torch.cuda.synchronize()
+    t_roll = time.perf_counter() - t0
+    stats = dict(model.last_stats)
+    t0 = time.perf_counter()
+    loss = grpo_loss_after_rollout(torch, pkg, model, toks, plens, lps, 32, 8)
+    torch.cuda.synchronize()
+    t_loss = time.perf_counter() - t0
+    generated = sum(len(x) for x in gen)
+    assert len(set(len(x) for x in toks)) == 1, "fixed-length rollout expected (no EOS)"
+    out.update(dict(generated=generated, rollout_s=t_roll, loss_s=t_loss, loss=loss,
+                    tokens_per_s=generated / t_roll, tokens_per_s_with_loss=generated / (t_roll + t_loss),
+                    num_blocks=model._num_blocks, **stats))
+    del model
+    torch.cuda.empty_cache()
+    return out
+
+
 def leg_copy_calibration(torch, dev, nbytes=1 << 30):
     """A plain device copy of known size, for scaling FETCH_SIZE / WRITE_SIZE."""
     src = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=dev).fill_(1)
@@ -242,7 +450,9 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--legs", default="decode,grpo,store,prefill")
+    ap.add_argument("--legs", default="decode,grpo,store,prefill,rollout")
+    ap.add_argument("--rollout-tokens", type=int, default=1024,
+                    help="new tokens per sequence in the end-to-end rollout leg")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 1 GiB device copy (counter calibration)")
@@ -269,19 +479,24 @@ def main() -> int:
 
     torch.cuda.synchronize()
     results = {}
+    cpu = None
     if "decode" in legs:
         results["decode"] = leg_decode(torch, pkg, W, dev, args.steps, args.warmup)
+        if not args.no_cpu:
+            log("cpu baseline (oracle decode)")
+            cpu = cpu_baseline_decode(torch, W, results["decode"]["workload"])
+        results["decode"]["kv_pool_gb"] = results["decode"]["workload"]["k_cache"].numel() * 4 / 1e9
+        del results["decode"]["workload"]
+        torch.cuda.empty_cache()
     if "grpo" in legs:
         results["grpo"] = leg_grpo(torch, pkg, W, dev, max(3, args.steps // 2), args.warmup)
     if "store" in legs:
         results["store"] = leg_store(torch, pkg, dev, args.steps, args.warmup)
     if "prefill" in legs:
         results["prefill"] = leg_prefill(torch, pkg, W, dev, max(3, args.steps // 2), args.warmup)
+    if "rollout" in legs:
+        results["rollout"] = leg_rollout(torch, pkg, dev, new_tokens=args.rollout_tokens)
 
-    cpu = None
-    if not args.no_cpu and "decode" in results:
-        log("cpu baseline (oracle decode)")
-        cpu = cpu_baseline_decode(torch, W, results["decode"]["workload"])
     cpu_grpo = None
     if not args.no_cpu and "grpo" in results:
         log("cpu baseline (oracle grpo)")
@@ -315,6 +530,27 @@ def main() -> int:
             "flops_per_layer": r["flops"], "causal_pairs": r["causal_pairs"],
             "chunk_steps": r["n_steps"], "query_tokens": r["q_tokens"]}
 
+    if "rollout" in results:
+        r = results["rollout"]
+        secondary["grpo_rollout"] = {
+            "workload": "random-init Qwen3-0.6B bf16, 32 prompts x group 8 = 256 seqs, 128-token "
+                        f"prompts, {args.rollout_tokens} new tokens, T=1.0, no top-k, continuous "
+                        "batching (2048-token budget, LIFO preemption), ~40 GB KV pool, then "
+                        "per-token logprob gather + group advantages + clipped loss",
+            "tokens_per_s": round(r["tokens_per_s"], 1),
+            "tokens_per_s_with_loss": round(r["tokens_per_s_with_loss"], 1),
+            "generated_tokens": r["generated"], "rollout_s": round(r["rollout_s"], 3),
+            "loss_s": round(r["loss_s"], 3), "loss": r["loss"], "kv_blocks": r["num_blocks"],
+            "preemptions": r.get("preemptions"), "engine_steps": r.get("steps"),
+            "graph_decode_steps": r.get("graph_steps"),
+            "short_compare_64_tokens": {
+                "ours_tokens_per_s": round(r["ours_short"], 1),
+                "reference_path_tokens_per_s": round(r["reference_path_short"], 1),
+                "reference_path": "same scheduler; torch RMSNorm/RoPE/SwiGLU/store; attention = "
+                                  f"{ReferencePath.attention_kind} over block-table-gathered K/V "
+                                  "(flash-attn unavailable); eager decode",
+                "speedup": round(r["ours_short"] / r["reference_path_short"], 2)}}
+
     if "decode" in results:
         d = results["decode"]
         line = {
@@ -335,7 +571,7 @@ def main() -> int:
                 "batch": 64, "context": "U{1024..4096}", "mean_context": round(d["mean_ctx"], 1),
                 "q_heads": 16, "kv_heads": 8, "head_dim": 128, "page_tokens": 256,
                 "layers": d["layers"],
-                "kv_pool_gb": round(d["workload"]["k_cache"].numel() * 2 * 2 / 1e9, 2)},
+                "kv_pool_gb": round(d["kv_pool_gb"], 2)},
             "roofline": {
                 "bound": "hbm", "achieved": round(d["launch_gbs"], 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(d["launch_gbs"] / HBM_PEAK_GBS, 4),
