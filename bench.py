@@ -33,6 +33,11 @@ if str(ROOT) not in sys.path:
 
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+# HBM bytes per decode launch (balanced split + merge) at the 28-layer B=64 shape,
+# measured by two rocprofv3 --pmc passes (FETCH_SIZE scaled by 2.0, WRITE_SIZE by
+# 1.0, the factors a plain copy of known size gives); recorded in
+# profiles/paged_decode_28layer_b64_ctx1024-4096.md.
+DECODE_TRAFFIC_BYTES = 672350105
 METRIC = "decode-attn HBM GB/s (% of 8 TB/s); GRPO rollout tokens/s on 1 GPU"
 
 
@@ -575,8 +580,11 @@ def main() -> int:
             "roofline": {
                 "bound": "hbm", "achieved": round(d["launch_gbs"], 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(d["launch_gbs"] / HBM_PEAK_GBS, 4),
-                "traffic": None,
-                "kernel": "paged_decode_split (+ paged_decode_merge)",
+                "traffic": DECODE_TRAFFIC_BYTES,
+                "traffic_note": "HBM bytes per launch (split + merge) from rocprofv3 FETCH_SIZE x2.0 "
+                                "+ WRITE_SIZE x1.0 passes of this leg, "
+                                "profiles/paged_decode_28layer_b64_ctx1024-4096.md",
+                "kernel": "decode_streamk_split<8,2> (+ decode_streamk_merge<8,2>)",
                 "us_per_launch": round(d["avg_launch_us"], 2),
                 "bytes_per_launch": d["bytes_per_launch"]},
             "cpu_baseline": cpu,

@@ -75,7 +75,13 @@ int qmi_store_kvcache(const uint16_t* key, int64_t key_row_stride,
  * workspace: fp32 scratch of at least qmi_paged_decode_workspace_bytes().
  * q head h reads KV head h / (num_q_heads / num_kv_heads).
  * Supported: head_dim 128, block_size 256, num_q_heads / num_kv_heads in
- * {1, 2, 4, 8}.  pages_per_split <= 0 chooses the split size automatically.
+ * {1, 2, 4, 8}.  pages_per_split <= 0 selects the balanced schedule (two
+ * workgroups per CU each stream an equal share of the keys over all KV
+ * heads; num_kv_heads in {2, 4, 8, 16}, ratio in {1, 2, 4}, batch <= 1024,
+ * out 16-byte aligned with strides a multiple of 8) when it applies, else an
+ * automatic per-(sequence, KV head) split; pages_per_split > 0 forces the
+ * per-(sequence, KV head) split with that many pages.  With
+ * pages_per_split <= 0 the workspace size covers either schedule.
  * Pages whose table entry is outside [0, num_blocks) contribute nothing.
  */
 int64_t qmi_paged_decode_workspace_bytes(int64_t batch, int64_t num_kv_heads,

@@ -311,6 +311,18 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 }  // namespace
 
+namespace qmi {
+// Balanced decode (paged_decode_streamk.hip).
+int64_t streamk_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                                int64_t bt_width);
+bool streamk_supported(int64_t num_q_heads, int64_t num_kv_heads, int64_t batch);
+int launch_streamk(const uint16_t* q, int64_t qs, int64_t qh, const uint16_t* kc,
+                   const uint16_t* vc, int64_t nb, int64_t num_q_heads, int64_t num_kv_heads,
+                   const int32_t* lens, int32_t bias, const int32_t* bt, int64_t bts, int64_t btw,
+                   int64_t batch, float scale, uint16_t* out, int64_t os, int64_t oh, float* ws,
+                   hipStream_t s);
+}  // namespace qmi
+
 extern "C" int64_t qmi_paged_decode_workspace_bytes(int64_t batch, int64_t num_kv_heads,
                                                     int64_t num_q_heads, int64_t bt_width,
                                                     int64_t pages_per_split) {
@@ -318,8 +330,16 @@ extern "C" int64_t qmi_paged_decode_workspace_bytes(int64_t batch, int64_t num_k
   const int64_t pps = pages_per_split > 0 ? pages_per_split
                                           : auto_pages_per_split(batch, num_kv_heads, bt_width);
   const int64_t num_splits = (bt_width + pps - 1) / pps;
-  if (num_splits <= 1) return 0;
-  return batch * num_q_heads * num_splits * kWsStride * (int64_t)sizeof(float);
+  const int64_t split_bytes =
+      num_splits <= 1 ? 0 : batch * num_q_heads * num_splits * kWsStride * (int64_t)sizeof(float);
+  // The automatic schedule may take either path (the balanced one needs a
+  // 16-byte aligned output), so it asks for the larger of the two.
+  if (pages_per_split <= 0 && num_q_heads % num_kv_heads == 0 &&
+      qmi::streamk_supported(num_q_heads, num_kv_heads, batch)) {
+    const int64_t sk = qmi::streamk_workspace_bytes(batch, num_q_heads, num_kv_heads, bt_width);
+    return sk > split_bytes ? sk : split_bytes;
+  }
+  return split_bytes;
 }
 
 extern "C" int qmi_paged_decode_attention(
@@ -344,12 +364,21 @@ extern "C" int qmi_paged_decode_attention(
     return QMI_E_BAD_STRIDE;
   const int64_t G = num_q_heads / num_kv_heads;
   if (G != 1 && G != 2 && G != 4 && G != 8) return QMI_E_UNSUPPORTED;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (pages_per_split <= 0 && qmi::streamk_supported(num_q_heads, num_kv_heads, batch) &&
+      aligned16(out) && out_seq_stride % 8 == 0 && out_head_stride % 8 == 0) {
+    const int64_t need = qmi::streamk_workspace_bytes(batch, num_q_heads, num_kv_heads, bt_width);
+    if (!workspace || workspace_bytes < need) return QMI_E_WORKSPACE_TOO_SMALL;
+    return qmi::launch_streamk(q, q_seq_stride, q_head_stride, k_cache, v_cache, num_blocks,
+                               num_q_heads, num_kv_heads, seqlens, seqlen_bias, block_table,
+                               bt_stride, bt_width, batch, scale, out, out_seq_stride,
+                               out_head_stride, workspace, s);
+  }
   const int64_t pps = pages_per_split > 0 ? pages_per_split
                                           : auto_pages_per_split(batch, num_kv_heads, bt_width);
   const int64_t need = qmi_paged_decode_workspace_bytes(batch, num_kv_heads, num_q_heads,
                                                         bt_width, pps);
   if (need > 0 && (!workspace || workspace_bytes < need)) return QMI_E_WORKSPACE_TOO_SMALL;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
 #define QMI_DECODE_CASE(GG)                                                                    \
   case GG:                                                                                     \
     return launch_decode<GG>(q, q_seq_stride, q_head_stride, k_cache, v_cache, num_blocks,     \

@@ -1,0 +1,451 @@
+// Paged GQA decode attention, balanced ("stream-K") variant for gfx950.
+//
+// Reference semantics: as paged_decode.hip (flash_attn_with_kvcache in
+// Qwen3Attention.forward_decode, qwen3_naive.py:672-680).
+//
+// Work decomposition.  The keys of all sequences are cut into steps of
+// 4 * (16 / Hkv) tokens (8 for 8 KV heads; a divisor of the 256-token page);
+// the flattened list of steps (sequence-major) is divided evenly over a fixed
+// grid of two workgroups per CU, so every workgroup streams the same number
+// of K/V bytes whatever the context lengths are (ragged batches leave no
+// tail of idle CUs).  Two workgroups per CU with 8 dwordx4 loads per lane in
+// flight read faster than more workgroups or deeper steps: on a 28-layer
+// B=64 sweep, 1024 workgroups x 16 loads ran at 5.5 TB/s, 512 x 8 at 6.15.
+// A workgroup handles every KV head of its tokens: lane l owns head-dim slice
+// [8*(l%16), +8) of KV head (l/16) % HKV for token group l / (16*HKV), and a
+// token group owns 8 consecutive tokens of the step, so each wave-wide
+// dwordx4 load reads 1 KB of a contiguous token row (all KV heads of a token
+// are adjacent in the [blocks, 256, Hkv, 128] cache).  Addresses are a
+// per-page scalar base plus a 32-bit lane offset, and the loads of a step are
+// issued unconditionally (a step never leaves its page); tokens past the
+// context are masked only in a sequence's last, partial step.
+// Per 16-lane DPP row the QK partial dots (v_dot2_f32_bf16) are summed with
+// DPP adds; each row keeps its own online-softmax state (fp32, log2 domain)
+// for the G query heads of its KV head, so the step loop needs no barrier.
+// When a workgroup leaves a sequence, the token groups are merged through
+// LDS; a sequence covered entirely by one workgroup is written directly,
+// otherwise the segment's (acc, m, l) go to one of the workgroup's two
+// partial slots (its first and its last segment) and the merge kernel
+// combines the slots of the workgroups that shared the sequence.
+#include "qmi_common.h"
+
+namespace {
+
+using namespace qmi;
+
+constexpr int kHeadDim = 128;
+constexpr int kPage = 256;
+constexpr int kThreads = 256;
+constexpr int kTok = 4;                        // tokens per lane per step
+// A workgroup of 256 lanes covers 16 lanes x HKV heads per token group.
+template <int HKV> constexpr int kTokGroups = 16 / HKV;
+template <int HKV> constexpr int kStepTokens = kTokGroups<HKV> * kTok;   // divides the page
+constexpr int kSlotStride = kHeadDim + 4;      // acc[128], m, l, pad (per q head)
+constexpr int kMaxSeqScan = 1024;              // batch limit of the in-LDS prefix scan
+
+__device__ __forceinline__ int64_t range_start(int64_t w, int64_t total, int64_t n_wg) {
+  return w * total / n_wg;
+}
+
+// Workgroup owning global step s: the largest w with range_start(w) <= s.
+__device__ __forceinline__ int64_t owner_of(int64_t s, int64_t total, int64_t n_wg) {
+  int64_t w = ((s + 1) * n_wg - 1) / total;
+  return w < n_wg - 1 ? w : n_wg - 1;
+}
+
+// Prefix sum of per-sequence step counts into LDS (exclusive; off[B] = total).
+// Each lane takes ceil(B / THREADS) consecutive sequences; lane sums are scanned
+// inside each wave with shuffles and across waves through LDS.
+template <int THREADS, int TS>
+__device__ void scan_steps(const int32_t* __restrict__ seqlens, int seqlen_bias, int bt_width,
+                           int batch, int* off) {
+  __shared__ int wave_tot[THREADS / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int per = (batch + THREADS - 1) / THREADS;
+  const int b0 = tid * per;
+  int mine = 0;
+  for (int i = 0; i < per; ++i) {
+    const int b = b0 + i;
+    if (b < batch) {
+      int L = seqlens[b] + seqlen_bias;
+      L = max(0, min(L, bt_width * kPage));
+      off[b] = mine;
+      mine += (L + TS - 1) / TS;
+    }
+  }
+  int incl = mine;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int t = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += t;
+  }
+  if (lane == 63) wave_tot[wave] = incl;
+  __syncthreads();
+  int base = incl - mine;
+  int total = 0;
+#pragma unroll
+  for (int wv = 0; wv < THREADS / 64; ++wv) {
+    if (wv < wave) base += wave_tot[wv];
+    total += wave_tot[wv];
+  }
+  for (int i = 0; i < per; ++i) {
+    const int b = b0 + i;
+    if (b < batch) off[b] += base;
+  }
+  if (tid == 0) off[batch] = total;
+  __syncthreads();
+}
+
+template <int HKV, int G>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(G <= 2 ? 4 : 2)))
+void decode_streamk_split(
+    const uint16_t* __restrict__ q, int64_t q_seq_stride, int64_t q_head_stride,
+    const uint16_t* __restrict__ k_cache, const uint16_t* __restrict__ v_cache,
+    int64_t num_blocks, const int32_t* __restrict__ seqlens, int seqlen_bias,
+    const int32_t* __restrict__ block_table, int64_t bt_stride, int bt_width, int batch,
+    int n_wg, float scale_log2, uint16_t* __restrict__ out, int64_t out_seq_stride,
+    int64_t out_head_stride, float* __restrict__ ws) {
+  constexpr int TG = kTokGroups<HKV>;
+  constexpr int TS = kStepTokens<HKV>;
+  constexpr int HQ = HKV * G;
+  constexpr int kRowBytes = HKV * kHeadDim * 2;          // one token of every KV head
+  constexpr int64_t kPageElems = (int64_t)kPage * HKV * kHeadDim;
+  __shared__ int off[kMaxSeqScan + 1];
+  __shared__ float sm_acc[TG][HKV][G][kHeadDim];
+  __shared__ float sm_ml[TG][HKV][G][2];
+
+  const int tid = threadIdx.x;
+  const int lane16 = tid & 15;
+  const int h = (tid >> 4) % HKV;
+  const int tg = tid / (16 * HKV);
+  const int64_t w = blockIdx.x;
+  // Byte offset of this lane's 16 B inside a step: token group tg owns the
+  // kTok consecutive tokens [tg*kTok, +kTok) of the step.
+  const uint32_t lane_off = (uint32_t)(tg * kTok * kRowBytes + (h * kHeadDim + lane16 * 8) * 2);
+
+  scan_steps<kThreads, TS>(seqlens, seqlen_bias, bt_width, batch, off);
+  const int64_t total = off[batch];
+  if (total == 0) return;
+  const int64_t s_begin = range_start(w, total, n_wg);
+  const int64_t s_end = range_start(w + 1, total, n_wg);
+  if (s_begin >= s_end) return;
+
+  // First sequence of the range (binary search over the exclusive offsets).
+  int lo = 0, hi = batch - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (off[mid] <= s_begin) lo = mid; else hi = mid - 1;
+  }
+  const int first_seq = lo;
+
+  int b = first_seq;
+  int64_t s = s_begin;
+  while (s < s_end) {
+    while (off[b + 1] <= s) ++b;  // skip empty sequences
+    const int64_t sb = off[b];
+    const int64_t seg_end = min((int64_t)off[b + 1], s_end);
+    int L = seqlens[b] + seqlen_bias;
+    L = max(0, min(L, bt_width * kPage));
+    const int32_t* bt_row = block_table + (int64_t)b * bt_stride;
+
+    uint32_t qw[G][4];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const uint4 v = load_u4(q + (int64_t)b * q_seq_stride +
+                              (int64_t)(h * G + g) * q_head_stride + lane16 * 8);
+      qw[g][0] = v.x; qw[g][1] = v.y; qw[g][2] = v.z; qw[g][3] = v.w;
+    }
+    float m[G], l[G], acc[G][8];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      m[g] = kNegBig;
+      l[g] = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+    }
+
+    // Page-table entry of the current page and the next one (prefetched so
+    // the lookup at a page change does not wait on memory).
+    int cur_page = (int)((s - sb) * TS / kPage);
+    int32_t blk = bt_row[cur_page];
+    int32_t blk_next = cur_page + 1 < bt_width ? bt_row[cur_page + 1] : -1;
+
+    for (int64_t st = s; st < seg_end; ++st) {
+      const int tok0 = (int)(st - sb) * TS;               // first token of the step
+      const int page = tok0 / kPage;
+      if (page != cur_page) {                             // wave-uniform
+        cur_page = page;
+        blk = blk_next;
+        blk_next = page + 1 < bt_width ? bt_row[page + 1] : -1;
+      }
+      const bool page_ok = blk >= 0 && blk < num_blocks;
+      const int n_valid = page_ok ? min(TS, L - tok0) : 0;
+      // Unmapped pages read page 0 (in bounds) and are masked below.
+      const int64_t pg = page_ok ? blk : 0;
+      const char* kp = reinterpret_cast<const char*>(k_cache + pg * kPageElems);
+      const char* vp = reinterpret_cast<const char*>(v_cache + pg * kPageElems);
+      const uint32_t o0 = (uint32_t)((tok0 % kPage) * kRowBytes) + lane_off;
+      // Loads never leave the page (steps are page-aligned), so they are
+      // issued unconditionally; tokens past the context are masked.
+      uint4 kr[kTok], vr[kTok];
+#pragma unroll
+      for (int i = 0; i < kTok; ++i) kr[i] = load_u4_stream(kp + (o0 + (uint32_t)(i * kRowBytes)));
+#pragma unroll
+      for (int i = 0; i < kTok; ++i) vr[i] = load_u4_stream(vp + (o0 + (uint32_t)(i * kRowBytes)));
+      const bool partial = n_valid < TS;                 // wave-uniform
+      if (partial) {
+#pragma unroll
+        for (int i = 0; i < kTok; ++i) {
+          const bool valid = tg * kTok + i < n_valid;
+          vr[i].x = valid ? vr[i].x : 0u;
+          vr[i].y = valid ? vr[i].y : 0u;
+          vr[i].z = valid ? vr[i].z : 0u;
+          vr[i].w = valid ? vr[i].w : 0u;
+        }
+      }
+      float sc[G][kTok];
+#pragma unroll
+      for (int i = 0; i < kTok; ++i) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          float d = dot2_bf16(qw[g][0], kr[i].x, 0.f);
+          d = dot2_bf16(qw[g][1], kr[i].y, d);
+          d = dot2_bf16(qw[g][2], kr[i].z, d);
+          d = dot2_bf16(qw[g][3], kr[i].w, d);
+          sc[g][i] = row16_sum(d) * scale_log2;
+        }
+      }
+      if (partial) {
+#pragma unroll
+        for (int i = 0; i < kTok; ++i) {
+          const bool valid = tg * kTok + i < n_valid;
+#pragma unroll
+          for (int g = 0; g < G; ++g) sc[g][i] = valid ? sc[g][i] : -INFINITY;
+        }
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float mx = sc[g][0];
+#pragma unroll
+        for (int i = 1; i < kTok; ++i) mx = fmaxf(mx, sc[g][i]);
+        const float mn = fmaxf(m[g], mx);
+        const float alpha = fast_exp2(m[g] - mn);
+        m[g] = mn;
+        l[g] *= alpha;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[g][e] *= alpha;
+#pragma unroll
+        for (int i = 0; i < kTok; ++i) {
+          const float p = fast_exp2(sc[g][i] - mn);
+          sc[g][i] = p;
+          l[g] += p;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < kTok; ++i) {
+        float v[8];
+        v[0] = bf16_lo(vr[i].x); v[1] = bf16_hi(vr[i].x);
+        v[2] = bf16_lo(vr[i].y); v[3] = bf16_hi(vr[i].y);
+        v[4] = bf16_lo(vr[i].z); v[5] = bf16_hi(vr[i].z);
+        v[6] = bf16_lo(vr[i].w); v[7] = bf16_hi(vr[i].w);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(sc[g][i], v[e], acc[g][e]);
+        }
+      }
+    }
+
+    // ---- merge the token groups of this segment through LDS ----
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sm_acc[tg][h][g][lane16 * 8 + e] = acc[g][e];
+      if (lane16 == 0) {
+        sm_ml[tg][h][g][0] = m[g];
+        sm_ml[tg][h][g][1] = l[g];
+      }
+    }
+    __syncthreads();
+    const bool whole = (s == sb) && (seg_end == off[b + 1]);
+    const int slot = (b == first_seq) ? 0 : 1;
+    for (int o = tid; o < HQ * kHeadDim; o += kThreads) {
+      const int qh = o / kHeadDim, d = o % kHeadDim;
+      const int hh = qh / G, g = qh % G;
+      float M = sm_ml[0][hh][g][0];
+#pragma unroll
+      for (int t = 1; t < TG; ++t) M = fmaxf(M, sm_ml[t][hh][g][0]);
+      float Ls = 0.f, A = 0.f;
+#pragma unroll
+      for (int t = 0; t < TG; ++t) {
+        const float a = fast_exp2(sm_ml[t][hh][g][0] - M);
+        Ls += sm_ml[t][hh][g][1] * a;
+        A += sm_acc[t][hh][g][d] * a;
+      }
+      if (whole) {
+        out[(int64_t)b * out_seq_stride + (int64_t)qh * out_head_stride + d] =
+            f32_to_bf16(Ls > 0.f ? A / Ls : 0.f);
+      } else {
+        float* p = ws + (((int64_t)w * 2 + slot) * HQ + qh) * kSlotStride;
+        p[d] = A;
+        if (d == 0) {
+          p[kHeadDim] = M;
+          p[kHeadDim + 1] = Ls;
+        }
+      }
+    }
+    __syncthreads();  // LDS is reused by the next segment
+    s = seg_end;
+  }
+}
+
+// Combines the partial slots of sequences shared by several workgroups and
+// writes zeros for empty sequences.  One workgroup per (sequence, query head):
+// 16 groups of 16 lanes take every 16th sharing workgroup (a lane owns 8
+// output dims), so the slot loads of up to 16 workgroups are in flight at
+// once; the 16 group states are then combined through LDS.
+template <int HKV, int G>
+__global__ __launch_bounds__(kThreads) void decode_streamk_merge(
+    const int32_t* __restrict__ seqlens, int seqlen_bias, int bt_width, int batch, int n_wg,
+    const float* __restrict__ ws, uint16_t* __restrict__ out, int64_t out_seq_stride,
+    int64_t out_head_stride) {
+  constexpr int HQ = HKV * G;
+  constexpr int kGroups = kThreads / 16;
+  __shared__ int off[kMaxSeqScan + 1];
+  __shared__ float s_ml[kGroups][2];
+  __shared__ float s_acc[kGroups][kHeadDim];
+  scan_steps<kThreads, kStepTokens<HKV>>(seqlens, seqlen_bias, bt_width, batch, off);
+  const int b = blockIdx.x, qh = blockIdx.y;
+  const int tid = threadIdx.x, lane16 = tid & 15, grp = tid >> 4;
+  uint16_t* o_row = out + (int64_t)b * out_seq_stride + (int64_t)qh * out_head_stride;
+  const int64_t total = off[batch];
+  const int64_t sb = off[b], se = off[b + 1];
+  if (se == sb) {  // empty sequence attends to nothing: zeros, as flash-attn
+    if (tid < kHeadDim) o_row[tid] = 0;
+    return;
+  }
+  const int64_t w0 = owner_of(sb, total, n_wg);
+  const int64_t w1 = owner_of(se - 1, total, n_wg);
+  if (w0 == w1) return;  // written directly by its only workgroup
+  const int d0 = lane16 * 8;
+  float M = kNegBig, Ls = 0.f, A[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) A[e] = 0.f;
+  for (int64_t ww = w0 + grp; ww <= w1; ww += kGroups) {
+    const int64_t r0 = range_start(ww, total, n_wg);
+    if (r0 == range_start(ww + 1, total, n_wg)) continue;  // empty range: owns no slot
+    const int slot = (r0 >= sb) ? 0 : 1;
+    const float* p = ws + ((ww * 2 + slot) * HQ + qh) * kSlotStride;
+    const float mw = p[kHeadDim], lw = p[kHeadDim + 1];
+    const f32x4_t a0 = *reinterpret_cast<const f32x4_t*>(p + d0);
+    const f32x4_t a1 = *reinterpret_cast<const f32x4_t*>(p + d0 + 4);
+    const float mn = fmaxf(M, mw);
+    const float s1 = fast_exp2(M - mn), s2 = fast_exp2(mw - mn);
+    Ls = Ls * s1 + lw * s2;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      A[e] = A[e] * s1 + a0[e] * s2;
+      A[4 + e] = A[4 + e] * s1 + a1[e] * s2;
+    }
+    M = mn;
+  }
+  if (lane16 == 0) {
+    s_ml[grp][0] = M;
+    s_ml[grp][1] = Ls;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s_acc[grp][d0 + e] = A[e];
+  __syncthreads();
+  if (tid < kHeadDim) {
+    float Mx = s_ml[0][0];
+#pragma unroll
+    for (int g2 = 1; g2 < kGroups; ++g2) Mx = fmaxf(Mx, s_ml[g2][0]);
+    float Lt = 0.f, At = 0.f;
+#pragma unroll
+    for (int g2 = 0; g2 < kGroups; ++g2) {
+      const float a = fast_exp2(s_ml[g2][0] - Mx);
+      Lt += s_ml[g2][1] * a;
+      At += s_acc[g2][tid] * a;
+    }
+    o_row[tid] = f32_to_bf16(Lt > 0.f ? At / Lt : 0.f);
+  }
+}
+
+}  // namespace
+
+namespace qmi {
+
+// Compute units of the current device (cached per device id).
+static int64_t device_cus() {
+  static int64_t cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
+// Workgroups of the balanced decode: two per CU, never more than the step
+// count can feed.
+int64_t streamk_workgroups(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                           int64_t bt_width) {
+  (void)num_q_heads;
+  const int64_t ts = (16 / num_kv_heads) * kTok;
+  const int64_t max_steps = batch * ((bt_width * kPage + ts - 1) / ts);
+  const int64_t target = 2 * device_cus();
+  return max_steps < target ? (max_steps < 1 ? 1 : max_steps) : target;
+}
+
+int64_t streamk_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                                int64_t bt_width) {
+  return streamk_workgroups(batch, num_q_heads, num_kv_heads, bt_width) * 2 * num_q_heads * kSlotStride * (int64_t)sizeof(float);
+}
+
+bool streamk_supported(int64_t num_q_heads, int64_t num_kv_heads, int64_t batch) {
+  if (batch > kMaxSeqScan) return false;
+  const int64_t g = num_q_heads / num_kv_heads;
+  const bool hkv_ok = num_kv_heads == 2 || num_kv_heads == 4 || num_kv_heads == 8 || num_kv_heads == 16;
+  return hkv_ok && (g == 1 || g == 2 || g == 4) && batch <= 65535;
+}
+
+template <int HKV, int G>
+static int launch(const uint16_t* q, int64_t qs, int64_t qh, const uint16_t* kc, const uint16_t* vc,
+                  int64_t nb, const int32_t* lens, int32_t bias, const int32_t* bt, int64_t bts,
+                  int64_t btw, int64_t batch, float scale_log2, uint16_t* out, int64_t os,
+                  int64_t oh, float* ws, hipStream_t s) {
+  const int64_t n_wg = streamk_workgroups(batch, HKV * G, HKV, btw);
+  hipLaunchKernelGGL((decode_streamk_split<HKV, G>), dim3((unsigned)n_wg), dim3(kThreads), 0, s, q,
+                     qs, qh, kc, vc, nb, lens, (int)bias, bt, bts, (int)btw, (int)batch, (int)n_wg,
+                     scale_log2, out, os, oh, ws);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL((decode_streamk_merge<HKV, G>), dim3((unsigned)batch, (unsigned)(HKV * G)),
+                     dim3(kThreads), 0, s,
+                     lens, (int)bias, (int)btw, (int)batch, (int)n_wg, ws, out, os, oh);
+  QMI_RETURN_LAUNCH_STATUS();
+}
+
+int launch_streamk(const uint16_t* q, int64_t qs, int64_t qh, const uint16_t* kc,
+                   const uint16_t* vc, int64_t nb, int64_t num_q_heads, int64_t num_kv_heads,
+                   const int32_t* lens, int32_t bias, const int32_t* bt, int64_t bts, int64_t btw,
+                   int64_t batch, float scale, uint16_t* out, int64_t os, int64_t oh, float* ws,
+                   hipStream_t s) {
+  const float sl = scale * kLog2e;
+  const int64_t g = num_q_heads / num_kv_heads;
+#define QMI_SK(HK, GG)                                                                         \
+  if (num_kv_heads == HK && g == GG)                                                           \
+    return launch<HK, GG>(q, qs, qh, kc, vc, nb, lens, bias, bt, bts, btw, batch, sl, out, os, oh, \
+                          ws, s);
+  QMI_SK(8, 2) QMI_SK(8, 1) QMI_SK(8, 4)
+  QMI_SK(4, 1) QMI_SK(4, 2) QMI_SK(4, 4)
+  QMI_SK(2, 1) QMI_SK(2, 2) QMI_SK(2, 4)
+  QMI_SK(16, 1) QMI_SK(16, 2) QMI_SK(16, 4)
+#undef QMI_SK
+  return QMI_E_UNSUPPORTED;
+}
+
+}  // namespace qmi

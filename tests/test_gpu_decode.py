@@ -148,3 +148,40 @@ def test_decode_rejects_bad_shapes(pkg, gpu):
                                            w["v_cache"].to(gpu)[:, :128].contiguous(),
                                            w["cache_seqlens"].to(gpu), w["block_tables"].to(gpu),
                                            0.1)
+
+
+def test_decode_balanced_schedule_ragged_with_empty(pkg, gpu):
+    """Balanced schedule: empty sequences in the middle, one-token sequences,
+    sequences spanning many workgroups and many sharing one workgroup."""
+    lens = [0, 1, 4096, 17, 0, 300, 2049, 1, 255, 256, 257, 3000, 0, 9]
+    w = _ragged(60, lens)
+    print("[decode] balanced ragged", flush=True)
+    out = _decode(pkg, gpu, w)
+    torch.cuda.synchronize()
+    assert out[0].abs().max().item() == 0.0 and out[4].abs().max().item() == 0.0
+    _check(out, w)
+
+
+def test_decode_balanced_schedule_large_batch(pkg, gpu):
+    """More sequences than one workgroup per sequence: 300 short contexts."""
+    g = torch.Generator().manual_seed(61)
+    lens = torch.randint(1, 700, (300,), generator=g).tolist()
+    w = _ragged(62, lens)
+    print("[decode] balanced 300 seqs", flush=True)
+    out = _decode(pkg, gpu, w)
+    torch.cuda.synchronize()
+    _check(out, w)
+
+
+@pytest.mark.parametrize("hq,hkv", [(2, 2), (8, 2), (4, 4), (16, 4), (8, 8), (32, 8),
+                                    (16, 16), (32, 16), (64, 16)])
+def test_decode_balanced_schedule_head_layouts(pkg, gpu, hq, hkv):
+    """Balanced schedule over every supported KV-head count and GQA ratio
+    (the step length is 4 * 16 / Hkv tokens, so each layout cuts pages
+    differently); contexts end mid-step, on step and on page boundaries."""
+    lens = [1, 7, 8, 9, 63, 64, 65, 255, 256, 257, 700, 1500]
+    w = _ragged(70 + hq + hkv, lens, hq=hq, hkv=hkv)
+    print(f"[decode] balanced layout {hq}/{hkv}", flush=True)
+    out = _decode(pkg, gpu, w)
+    torch.cuda.synchronize()
+    _check(out, w)
