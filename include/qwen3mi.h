@@ -82,7 +82,8 @@ int qmi_store_kvcache(const uint16_t* key, int64_t key_row_stride,
  * automatic per-(sequence, KV head) split; pages_per_split > 0 forces the
  * per-(sequence, KV head) split with that many pages.  With
  * pages_per_split <= 0 the workspace size covers either schedule.
- * Pages whose table entry is outside [0, num_blocks) contribute nothing.
+ * Pages whose table entry is outside [0, num_blocks) contribute nothing;
+ * num_blocks == 0 is rejected (QMI_E_BAD_SHAPE).
  */
 int64_t qmi_paged_decode_workspace_bytes(int64_t batch, int64_t num_kv_heads,
                                          int64_t num_q_heads, int64_t bt_width,
@@ -115,7 +116,9 @@ int qmi_paged_decode_attention(const uint16_t* q, int64_t q_seq_stride, int64_t 
  * keys j <= i + Lk - Lq (new tokens see the whole cached prefix).
  * max_seqlen_q bounds Lq (it sizes the grid).  Query rows outside
  * [0, total_q) are never read or written.  Supported: head_dim 128,
- * block_size 256, num_q_heads / num_kv_heads in {1, 2, 4}.
+ * block_size 256, num_q_heads / num_kv_heads in {1, 2, 4}.  Keys on pages
+ * whose table entry is outside [0, num_blocks) contribute nothing (as in
+ * decode); num_blocks == 0 is rejected (QMI_E_BAD_SHAPE).
  */
 int qmi_varlen_prefill_attention(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride,
                                  const uint16_t* k_cache, const uint16_t* v_cache,

@@ -351,6 +351,7 @@ extern "C" int qmi_paged_decode_attention(
     int64_t workspace_bytes, int64_t pages_per_split, void* stream) {
   if (batch < 0 || num_blocks < 0 || bt_width < 0) return QMI_E_BAD_SHAPE;
   if (batch == 0) return QMI_OK;
+  if (num_blocks == 0) return QMI_E_BAD_SHAPE;  // a pool without pages
   if (!q || !k_cache || !v_cache || !seqlens || !block_table || !out) return QMI_E_NULL_POINTER;
   if (head_dim != kHeadDim || block_size != kPage) return QMI_E_UNSUPPORTED;
   if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads != 0)

@@ -10,16 +10,22 @@
 // sees keys j <= i + Lk - Lq.  Query head h reads KV head h / G.
 //
 // Design (FlashAttention-2 forward, reorganised for CDNA MFMA operands):
-//   * Workgroup = 4 wave64 = one (sequence, KV head, block of 64/G queries);
-//     wave w takes query head (w / (4/G)) of the GQA group and 16 queries, so
-//     the K/V tiles staged in LDS serve all G query heads.
+//   * Workgroup = 4 wave64 = one (sequence, KV head, block of 128/G queries);
+//     wave w takes query head (w / (4/G)) of the GQA group and 32 queries
+//     (two 16-query column blocks), so each K / V^T operand read from LDS
+//     feeds two MFMAs and the K/V tiles staged in LDS serve all G heads.
 //   * Scores are computed transposed, S^T = K Q^T, with
 //     v_mfma_f32_16x16x32_bf16 (A = 16 keys x 32 dims from LDS, B = Q^T held
 //     in registers).  Its accumulator layout (lane l: keys 4*(l/16)+r,
 //     query l%16) is exactly the B-operand layout of the second product
 //     O^T = V^T P^T once two 16-key blocks are packed to bf16, so P never
-//     leaves registers.  V^T comes from LDS, where each 64-key V tile is
-//     written transposed while being staged.
+//     leaves registers.
+//   * V^T lives in LDS with the keys of each 32-key chunk permuted so that
+//     the 8 keys one lane needs for a V^T operand (keys 32c+4g..+3 and
+//     32c+16+4g..+3) are contiguous: one 16-byte LDS read per operand.
+//     Staging: a lane loads 4 consecutive keys x 8 dims, transposes them in
+//     registers and writes 8 x 8 bytes (one per dim); the 16 lanes of a
+//     write phase cover one dim row, so the writes do not conflict.
 //   * Online softmax in fp32 (log2 domain); per query the 4 lanes holding
 //     its keys agree on the running max through two shuffles, while the
 //     running sum stays lane-partial until the end.
@@ -39,17 +45,24 @@ constexpr int kHeadDim = 128;
 constexpr int kPage = 256;
 constexpr int kThreads = 256;
 constexpr int kKeyTile = 64;
-constexpr int kKPitch = kHeadDim + 8;   // bf16 per K row in LDS (272 B, breaks bank aliasing)
-constexpr int kVtPitch = kKeyTile + 4;  // bf16 per V^T row in LDS (136 B)
-
-typedef __attribute__((ext_vector_type(2))) uint32_t u32x2_t;
+constexpr int kWaveQ = 32;              // queries per wave (two MFMA column blocks)
+constexpr int kKPitch = kHeadDim + 8;   // bf16 per K row in LDS (272 B: 16 rows hit 16 distinct 4-bank groups)
+constexpr int kVtPitch = kKeyTile + 8;  // bf16 per V^T row in LDS (144 B, 16-B aligned rows)
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
   return __builtin_bit_cast(bf16x8_t, u32x4_t{v.x, v.y, v.z, v.w});
 }
 
+// LDS position of key kk (0..63) inside a V^T row: within each 32-key chunk,
+// key 16h + 4g + r goes to 8g + 4h + r.
+__device__ __forceinline__ int vt_pos(int kk) {
+  const int c = kk >> 5, h = (kk >> 4) & 1, g = (kk >> 2) & 3, r = kk & 3;
+  return 32 * c + 8 * g + 4 * h + r;
+}
+
 template <int G>
-__global__ __launch_bounds__(kThreads) void varlen_prefill_kernel(
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void varlen_prefill_kernel(
     const uint16_t* __restrict__ q, int64_t q_tok_stride, int64_t q_head_stride,
     const uint16_t* __restrict__ k_cache, const uint16_t* __restrict__ v_cache,
     int64_t num_blocks, int num_kv_heads,
@@ -58,7 +71,7 @@ __global__ __launch_bounds__(kThreads) void varlen_prefill_kernel(
     int n_qblocks, int64_t total_q, float scale_log2,
     uint16_t* __restrict__ out, int64_t out_tok_stride, int64_t out_head_stride) {
   constexpr int kWavesPerHead = 4 / G;
-  constexpr int kQB = 16 * kWavesPerHead;  // queries per workgroup
+  constexpr int kQB = kWaveQ * kWavesPerHead;  // queries per workgroup
   __shared__ __attribute__((aligned(16))) uint16_t sK[2][kKeyTile * kKPitch];
   __shared__ __attribute__((aligned(16))) uint16_t sVt[2][kHeadDim * kVtPitch];
 
@@ -81,41 +94,64 @@ __global__ __launch_bounds__(kThreads) void varlen_prefill_kernel(
   const int diag = Lk - Lq;  // query i sees keys j <= i + diag
 
   const int qh = kvh * G + wave / kWavesPerHead;
-  const int wq0 = q0 + (wave % kWavesPerHead) * 16;
-  const int my_q = wq0 + l16;  // this lane's query (column of S^T)
-  const bool q_valid = my_q < Lq;
+  const int wq0 = q0 + (wave % kWavesPerHead) * kWaveQ;
 
-  // Q^T operand: lane holds Q[my_q][32c + 8*g4 .. +8] for c = 0..3.
-  bf16x8_t qop[4];
+  // Q^T operands: lane holds Q[query][32c + 8*g4 .. +8] for its query in
+  // column block j (query wq0 + 16j + l16) and c = 0..3.
+  bf16x8_t qop[2][4];
+  int my_pos[2];  // last key each of this lane's queries may see (-1: none)
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (q_valid)
-      v = load_u4(q + (int64_t)(q_start + my_q) * q_tok_stride + (int64_t)qh * q_head_stride +
-                  32 * c + 8 * g4);
-    qop[c] = as_bf16x8(v);
+  for (int j = 0; j < 2; ++j) {
+    const int my_q = wq0 + 16 * j + l16;
+    const bool ok = my_q < Lq;
+    my_pos[j] = ok ? diag + my_q : -1;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (ok)
+        v = load_u4(q + (int64_t)(q_start + my_q) * q_tok_stride + (int64_t)qh * q_head_stride +
+                    32 * c + 8 * g4);
+      qop[j][c] = as_bf16x8(v);
+    }
   }
 
   // Keys this workgroup needs: up to the last query's diagonal.
   const int kend = max(0, min(Lk, diag + min(q0 + kQB, Lq)));
   const int n_tiles = (kend + kKeyTile - 1) / kKeyTile;
 
-  // Staging: each lane moves 4 K chunks and 4 V chunks of 16 B per tile.
+  // Staging.  K: lane moves chunks c = tid + 256 i (key c / 16, dims
+  // 8 * (c % 16)), 256 contiguous bytes per 16 lanes.  V: lane (dc = tid / 16,
+  // kq = tid % 16) moves keys 4 kq .. 4 kq + 3 of dims 8 dc .. 8 dc + 7.
+  // Addresses are a per-tile scalar base (the tile's first key row of this KV
+  // head) plus a fixed 32-bit lane offset.  A tile never leaves its page, so
+  // the loads are issued unconditionally; keys at or past kend are stale page
+  // rows, masked in the scores, and their V rows are zeroed.  A tile whose
+  // page-table entry is outside [0, num_blocks) is skipped in the compute.
+  const int64_t row_elems = (int64_t)num_kv_heads * kHeadDim;
+  uint32_t k_off[4], v_off[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = tid + kThreads * i;
+    k_off[i] = (uint32_t)(((c >> 4) * row_elems + 8 * (c & 15)) * 2);
+  }
+  const int v_dc = tid >> 4, v_kq = tid & 15;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v_off[i] = (uint32_t)(((4 * v_kq + i) * row_elems + 8 * v_dc) * 2);
   uint4 kst[4], vst[4];
+  bool tile_ok[2] = {false, false};
+  int st_valid = 0;  // valid keys in the staged tile
   auto load_tile = [&](int t) {
     const int key0 = t * kKeyTile;
-    const int64_t blk = block_table[(int64_t)b * bt_stride + key0 / kPage];
+    const int32_t blk = block_table[(int64_t)b * bt_stride + key0 / kPage];
     const bool page_ok = blk >= 0 && blk < num_blocks;
+    const int64_t row0 = (int64_t)(page_ok ? blk : 0) * kPage + (key0 % kPage);
+    const char* kb = reinterpret_cast<const char*>(k_cache + row0 * row_elems + kvh * kHeadDim);
+    const char* vb = reinterpret_cast<const char*>(v_cache + row0 * row_elems + kvh * kHeadDim);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = tid + kThreads * i;
-      const int key = c >> 4, dchunk = c & 15;
-      const bool ok = page_ok && (key0 + key) < kend;
-      const int64_t off = ((blk * kPage + (key0 % kPage) + key) * num_kv_heads + kvh) * kHeadDim +
-                          8 * dchunk;
-      kst[i] = ok ? load_u4(k_cache + off) : make_uint4(0, 0, 0, 0);
-      vst[i] = ok ? load_u4(v_cache + off) : make_uint4(0, 0, 0, 0);
-    }
+    for (int i = 0; i < 4; ++i) kst[i] = load_u4(kb + k_off[i]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) vst[i] = load_u4(vb + v_off[i]);
+    st_valid = page_ok ? min(kKeyTile, kend - key0) : 0;
   };
   auto store_tile = [&](int buf) {
 #pragma unroll
@@ -123,22 +159,38 @@ __global__ __launch_bounds__(kThreads) void varlen_prefill_kernel(
       const int c = tid + kThreads * i;
       const int key = c >> 4, dchunk = c & 15;
       *reinterpret_cast<uint4*>(&sK[buf][key * kKPitch + 8 * dchunk]) = kst[i];
-      const uint32_t w[4] = {vst[i].x, vst[i].y, vst[i].z, vst[i].w};
+    }
+    if (st_valid < kKeyTile) {  // wave-uniform: zero V rows past the valid keys
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        sVt[buf][(8 * dchunk + 2 * e) * kVtPitch + key] = (uint16_t)(w[e] & 0xffffu);
-        sVt[buf][(8 * dchunk + 2 * e + 1) * kVtPitch + key] = (uint16_t)(w[e] >> 16);
-      }
+      for (int i = 0; i < 4; ++i)
+        if (4 * v_kq + i >= st_valid) vst[i] = make_uint4(0, 0, 0, 0);
+    }
+    tile_ok[buf] = st_valid > 0;
+    const int pos = vt_pos(4 * v_kq);
+    const uint32_t w0[4] = {vst[0].x, vst[0].y, vst[0].z, vst[0].w};
+    const uint32_t w1[4] = {vst[1].x, vst[1].y, vst[1].z, vst[1].w};
+    const uint32_t w2[4] = {vst[2].x, vst[2].y, vst[2].z, vst[2].w};
+    const uint32_t w3[4] = {vst[3].x, vst[3].y, vst[3].z, vst[3].w};
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      // dims 8dc+2d (low halves) and 8dc+2d+1 (high halves) of keys 4kq..4kq+3
+      const uint32_t lo_e = __builtin_amdgcn_perm(w1[d], w0[d], 0x05040100u);
+      const uint32_t hi_e = __builtin_amdgcn_perm(w3[d], w2[d], 0x05040100u);
+      const uint32_t lo_o = __builtin_amdgcn_perm(w1[d], w0[d], 0x07060302u);
+      const uint32_t hi_o = __builtin_amdgcn_perm(w3[d], w2[d], 0x07060302u);
+      *reinterpret_cast<uint2*>(&sVt[buf][(8 * v_dc + 2 * d) * kVtPitch + pos]) = make_uint2(lo_e, hi_e);
+      *reinterpret_cast<uint2*>(&sVt[buf][(8 * v_dc + 2 * d + 1) * kVtPitch + pos]) =
+          make_uint2(lo_o, hi_o);
     }
   };
 
-  float m_run = kNegBig;  // running max (log2 domain) of this lane's query
-  float l_run = 0.f;      // lane-partial running sum
-  f32x4_t acc_o[8];       // O^T[dim 16*db + 4*g4 + r][query l16]
+  float m_run[2] = {kNegBig, kNegBig};  // running max (log2 domain) per query
+  float l_run[2] = {0.f, 0.f};          // lane-partial running sums
+  f32x4_t acc_o[2][8];                  // O^T[dim 16*db + 4*g4 + r][query]
 #pragma unroll
-  for (int db = 0; db < 8; ++db) acc_o[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  const int my_pos = diag + my_q;  // last key this query may see
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int db = 0; db < 8; ++db) acc_o[j][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   if (n_tiles > 0) {
     load_tile(0);
@@ -148,91 +200,139 @@ __global__ __launch_bounds__(kThreads) void varlen_prefill_kernel(
 
   for (int t = 0; t < n_tiles; ++t) {
     const int buf = t & 1;
+    const bool compute = tile_ok[buf];  // wave-uniform
     if (t + 1 < n_tiles) load_tile(t + 1);
+    if (compute) {
 
-    // ---- S^T = K Q^T for 4 blocks of 16 keys ----
-    f32x4_t s[4];
+    // ---- S^T = K Q^T for 4 blocks of 16 keys x 2 blocks of 16 queries ----
+    // The K operands of dim slice c+1 are read from LDS while the MFMAs of
+    // slice c run.
+    f32x4_t s[2][4];
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      f32x4_t a = {0.f, 0.f, 0.f, 0.f};
-      const uint16_t* krow = &sK[buf][(kb * 16 + l16) * kKPitch + 8 * g4];
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const bf16x8_t kop = as_bf16x8(*reinterpret_cast<const uint4*>(krow + 32 * c));
-        a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[c], a, 0, 0, 0);
+      for (int kb = 0; kb < 4; ++kb) s[j][kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const uint16_t* kbase = &sK[buf][l16 * kKPitch + 8 * g4];
+    bf16x8_t kop[2][4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+      kop[0][kb] = as_bf16x8(*reinterpret_cast<const uint4*>(kbase + kb * 16 * kKPitch));
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if (c + 1 < 4) {
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+          kop[(c + 1) & 1][kb] = as_bf16x8(
+              *reinterpret_cast<const uint4*>(kbase + kb * 16 * kKPitch + 32 * (c + 1)));
       }
-      s[kb] = a;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          s[j][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[c & 1][kb], qop[j][c], s[j][kb],
+                                                             0, 0, 0);
     }
 
-    // ---- scale, causal / length mask, tile max ----
+    // ---- per query block: mask, online softmax, P^T packed to bf16 ----
+    // Scores stay unscaled; p = exp2(s * scale_log2 - m).  The running max m
+    // (scaled domain) is only raised when a tile's max exceeds it by more
+    // than 8, so p <= 2^8 and the accumulator rescale is skipped on most
+    // tiles (the final division uses the same m, so the result is exact).
     const int key_base = t * kKeyTile;
-    float tmax = -INFINITY;
+    // Whole tile visible to every query of this wave: no masking needed.
+    const bool full = key_base + kKeyTile - 1 <= diag + wq0 && key_base + kKeyTile <= Lk &&
+                      wq0 + kWaveQ <= Lq;
+    bf16x8_t pop[2][2];
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
+    for (int j = 0; j < 2; ++j) {
+      if (!full) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = key_base + kb * 16 + 4 * g4 + r;
-        const bool ok = q_valid && key <= my_pos && key < Lk;
-        const float v = ok ? s[kb][r] * scale_log2 : -INFINITY;
-        s[kb][r] = v;
-        tmax = fmaxf(tmax, v);
+        for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int key = key_base + kb * 16 + 4 * g4 + r;
+            const bool ok = key <= my_pos[j] && key < Lk;
+            s[j][kb][r] = ok ? s[j][kb][r] : -INFINITY;
+          }
+        }
       }
-    }
-    tmax = fmaxf(tmax, shfl_xor_f32(tmax, 16));
-    tmax = fmaxf(tmax, shfl_xor_f32(tmax, 32));
-    const float m_new = fmaxf(m_run, tmax);
-    const float alpha = fast_exp2(m_run - m_new);
-    m_run = m_new;
-    l_run *= alpha;
+      float tmax = fmaxf(fmaxf(s[j][0][0], s[j][0][1]), fmaxf(s[j][0][2], s[j][0][3]));
 #pragma unroll
-    for (int db = 0; db < 8; ++db) acc_o[db] *= alpha;
-
-    // ---- P^T as bf16 B operands: chunk c packs key blocks 2c and 2c+1 ----
-    bf16x8_t pop[2];
+      for (int kb = 1; kb < 4; ++kb)
+        tmax = fmaxf(tmax, fmaxf(fmaxf(s[j][kb][0], s[j][kb][1]), fmaxf(s[j][kb][2], s[j][kb][3])));
+      tmax = fmaxf(tmax, shfl_xor_f32(tmax, 16));
+      tmax = fmaxf(tmax, shfl_xor_f32(tmax, 32));
+      const float m_cand = tmax * scale_log2;
+      const bool need = m_cand > m_run[j] + 8.f;
+      if (__ballot(need) != 0ull) {  // wave-uniform
+        const float m_new = need ? m_cand : m_run[j];
+        const float alpha = fast_exp2(m_run[j] - m_new);
+        m_run[j] = m_new;
+        l_run[j] *= alpha;
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      float p[8];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        p[r] = fast_exp2(s[2 * c][r] - m_new);
-        p[4 + r] = fast_exp2(s[2 * c + 1][r] - m_new);
+        for (int db = 0; db < 8; ++db) acc_o[j][db] *= alpha;
       }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        l_run += p[e];
-        pop[c][e] = (__bf16)p[e];
-      }
-    }
-
-    // ---- O^T += V^T P^T over 8 blocks of 16 dims ----
-#pragma unroll
-    for (int db = 0; db < 8; ++db) {
-      const uint16_t* vrow = &sVt[buf][(db * 16 + l16) * kVtPitch];
+      const float neg_m = -m_run[j];
+      // chunk c packs key blocks 2c and 2c+1
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(vrow + 32 * c + 4 * g4);
-        const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vrow + 32 * c + 16 + 4 * g4);
-        const u32x4_t w = {lo.x, lo.y, hi.x, hi.y};
-        acc_o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, w),
-                                                            pop[c], acc_o[db], 0, 0, 0);
+        float p[8];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          p[r] = fast_exp2(fmaf(s[j][2 * c][r], scale_log2, neg_m));
+          p[4 + r] = fast_exp2(fmaf(s[j][2 * c + 1][r], scale_log2, neg_m));
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          l_run[j] += p[e];
+          pop[j][c][e] = (__bf16)p[e];
+        }
       }
     }
 
+    // ---- O^T += V^T P^T over 8 blocks of 16 dims (operands read one block ahead) ----
+    const uint16_t* vbase = &sVt[buf][l16 * kVtPitch + 8 * g4];
+    bf16x8_t vop[2][2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+      vop[0][c] = as_bf16x8(*reinterpret_cast<const uint4*>(vbase + 32 * c));
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+      if (db + 1 < 8) {
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+          vop[(db + 1) & 1][c] = as_bf16x8(*reinterpret_cast<const uint4*>(
+              vbase + (db + 1) * 16 * kVtPitch + 32 * c));
+      }
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc_o[j][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop[db & 1][c], pop[j][c],
+                                                                 acc_o[j][db], 0, 0, 0);
+    }
+
+    }  // compute
     if (t + 1 < n_tiles) store_tile(buf ^ 1);
     __syncthreads();
   }
 
   // ---- normalise and write O[query][dims] ----
-  float l_tot = l_run + shfl_xor_f32(l_run, 16);
-  l_tot += shfl_xor_f32(l_tot, 32);
-  const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-  if (q_valid) {
-    uint16_t* orow = out + (int64_t)(q_start + my_q) * out_tok_stride + (int64_t)qh * out_head_stride;
 #pragma unroll
-    for (int db = 0; db < 8; ++db) {
-      const uint32_t w0 = pack_bf16x2(acc_o[db][0] * inv, acc_o[db][1] * inv);
-      const uint32_t w1 = pack_bf16x2(acc_o[db][2] * inv, acc_o[db][3] * inv);
-      *reinterpret_cast<u32x2_t*>(orow + db * 16 + 4 * g4) = u32x2_t{w0, w1};
+  for (int j = 0; j < 2; ++j) {
+    float l_tot = l_run[j] + shfl_xor_f32(l_run[j], 16);
+    l_tot += shfl_xor_f32(l_tot, 32);
+    const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+    const int my_q = wq0 + 16 * j + l16;
+    if (my_q < Lq) {
+      uint16_t* orow =
+          out + (int64_t)(q_start + my_q) * out_tok_stride + (int64_t)qh * out_head_stride;
+#pragma unroll
+      for (int db = 0; db < 8; ++db) {
+        const uint32_t w0 = pack_bf16x2(acc_o[j][db][0] * inv, acc_o[j][db][1] * inv);
+        const uint32_t w1 = pack_bf16x2(acc_o[j][db][2] * inv, acc_o[j][db][3] * inv);
+        *reinterpret_cast<uint2*>(orow + db * 16 + 4 * g4) = make_uint2(w0, w1);
+      }
     }
   }
 }
@@ -251,6 +351,7 @@ extern "C" int qmi_varlen_prefill_attention(
   if (batch < 0 || max_seqlen_q < 0 || num_blocks < 0 || bt_width < 0) return QMI_E_BAD_SHAPE;
   if (total_q < 0) return QMI_E_BAD_SHAPE;
   if (batch == 0 || max_seqlen_q == 0 || total_q == 0) return QMI_OK;
+  if (num_blocks == 0) return QMI_E_BAD_SHAPE;  // a pool without pages
   if (!q || !k_cache || !v_cache || !cu_seqlens_q || !cu_seqlens_k || !block_table || !out)
     return QMI_E_NULL_POINTER;
   if (head_dim != kHeadDim || block_size != kPage) return QMI_E_UNSUPPORTED;
@@ -263,7 +364,7 @@ extern "C" int qmi_varlen_prefill_attention(
       !aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) ||
       (reinterpret_cast<uintptr_t>(out) & 7u))
     return QMI_E_BAD_STRIDE;
-  const int64_t qb = 64 / G;
+  const int64_t qb = 128 / G;
   const int64_t n_qblocks = (max_seqlen_q + qb - 1) / qb;
   if (n_qblocks > 65535 || batch > 65535 || num_kv_heads > 65535 || bt_width > (1 << 22))
     return QMI_E_UNSUPPORTED;

@@ -184,3 +184,28 @@ def test_prefill_rejects_bad_inputs(pkg, gpu):
     with pytest.raises(ValueError):
         pkg.kernels.varlen_prefill_attention(q, kc.to(gpu), vc.to(gpu), cq, cq, 10, 10, SCALE,
                                              True, None)
+
+
+def test_prefill_unmapped_page_contributes_nothing(pkg, gpu):
+    """Keys on a page whose table entry is -1 are ignored, as in decode: 8
+    queries at the end of a 300-key sequence whose second page is unmapped
+    attend exactly to the 256 keys of the first page (each query's causal
+    horizon is past key 255), which is decode attention over that page."""
+    kc, vc, bt = _pool(90, [300])
+    bt[0, 1] = -1
+    g = torch.Generator().manual_seed(91)
+    q = torch.randn(8, 16, 128, generator=g).to(torch.bfloat16)
+    print("[prefill] unmapped page", flush=True)
+    out = _run(pkg, gpu, q, kc, vc, [0, 8], [0, 300], bt)
+    ref = OA.paged_decode(q, kc, vc, torch.full((8,), 256, dtype=torch.int32),
+                          bt[:, :1].repeat(8, 1), SCALE)
+    assert (out.float().cpu() - ref).abs().max().item() <= TOL
+
+
+def test_prefill_rejects_empty_pool(pkg, gpu):
+    kc = torch.zeros(0, 256, 8, 128, dtype=torch.bfloat16, device=gpu)
+    q = torch.zeros(4, 16, 128, dtype=torch.bfloat16, device=gpu)
+    cu = torch.tensor([0, 4], dtype=torch.int32, device=gpu)
+    bt = torch.zeros(1, 1, dtype=torch.int32, device=gpu)
+    with pytest.raises((ValueError, RuntimeError)):
+        pkg.kernels.varlen_prefill_attention(q, kc, kc, cu, cu, 4, 4, SCALE, True, bt)
