@@ -274,6 +274,24 @@ int qmi_logprob_gather_backward(const uint16_t* logits, int64_t logit_seq_stride
                                 uint16_t* grad, int64_t grad_seq_stride, int64_t grad_tok_stride,
                                 void* stream);
 
+/*
+ * Token sampling with the drawn token's log-probability, one pass over bf16
+ * logits rows.  Replaces, for top_k = None, the sampling step of
+ * generate_continuous (qwen3_naive.py:1413-1423) and of
+ * generate_continuous_with_logprobs (:1636-1650):
+ *   x = logits.float() / temperature; tok ~ Categorical(softmax(x));
+ *   lp = log_softmax(x)[tok].
+ * Draw: Gumbel-max with Philox4x32-10 uniforms; element i of row r uses word
+ * i % 4 of the block at counter (i / 4, r, offset_lo, offset_hi), key
+ * (seed_lo, seed_hi); a given (seed, offset) reproduces the same tokens.
+ * logits: [n_rows, vocab] bf16 with row stride row_stride (elements).
+ * out_tokens: int64 [n_rows]; out_logprobs: fp32 [n_rows] or NULL.
+ * temperature must be finite and > 0.
+ */
+int qmi_sample_tokens(const uint16_t* logits, int64_t row_stride, int64_t n_rows, int64_t vocab,
+                      float temperature, uint64_t seed, uint64_t offset, int64_t* out_tokens,
+                      float* out_logprobs, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

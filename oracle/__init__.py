@@ -19,5 +19,9 @@ Modules and what pins each one (the checks live in tests/test_oracle_*.py):
   norm_rope  RMSNorm, add+RMSNorm, RoPE cache and rotation
              -> torch rms_norm (library), complex-rotation restatement,
                 norm preservation, position-0 identity.
+  sampling   temperature softmax draw + log-probability of the drawn token
+             (Gumbel-max over Philox4x32-10 uniforms)
+             -> Philox known-answer vectors of its authors, chi-square of
+                the drawn frequencies against softmax, torch.log_softmax.
   workloads  seeded synthetic inputs for the five benchmark configurations.
 """

@@ -1,0 +1,185 @@
+// Token sampling from bf16 logits in one streaming pass: temperature,
+// softmax, the categorical draw and the drawn token's log-probability.
+//
+// Reference semantics (qwen3_naive.py, generate_continuous :1413-1423 and
+// generate_continuous_with_logprobs :1636-1650, top_k = None):
+//   x = logits.float() / T;  tok ~ Categorical(softmax(x));  lp = log_softmax(x)[tok]
+//
+// Method: Gumbel-max.  tok = argmax_i (x_i + G_i) with G_i iid Gumbel(0, 1)
+// has exactly the softmax(x) distribution.  G_i = -ln(-ln U_i), where U_i is
+// the (i % 4)-th word of Philox4x32-10 (Salmon, Moraes, Dror and Shaw,
+// "Parallel random numbers: as easy as 1, 2, 3", SC 2011) at counter
+// (i / 4, row, offset_lo, offset_hi) and key (seed_lo, seed_hi), mapped to
+// ((w >> 8) + 0.5) / 2^24, strictly inside (0, 1).  Scores are kept in log2
+// units, s_i = x_i log2(e) - log2(-log2 U_i), a positive scaling plus a
+// constant shift of x_i + G_i, so the argmax is the same; E = -ln U is
+// taken from 1 - U near U = 1 so the large Gumbel values keep full
+// precision.  Ties go to the lowest index.  The same pass keeps the row's
+// online log-sum-exp, so
+// lp = (x_tok log2(e) - lse2) ln 2 needs one extra load of logits[tok].
+//
+// gfx950 design: one 256-lane workgroup per row, 16-byte non-temporal loads
+// (8 logits), two Philox blocks per load; per-lane (max, sum of exp2) and
+// (best score, index) merged with shuffles and one LDS exchange.
+#include "qmi_common.h"
+
+namespace {
+
+using namespace qmi;
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+
+__device__ __forceinline__ uint4 philox4x32_10(uint4 c, uint32_t k0, uint32_t k1) {
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    const uint32_t lo0 = 0xD2511F53u * c.x, hi0 = __umulhi(0xD2511F53u, c.x);
+    const uint32_t lo1 = 0xCD9E8D57u * c.z, hi1 = __umulhi(0xCD9E8D57u, c.z);
+    c = make_uint4(hi1 ^ c.y ^ k0, lo1, hi0 ^ c.w ^ k1, lo0);
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+  return c;
+}
+
+// Gumbel term in log2 units: -log2(E log2 e) with E = -ln U,
+// U = ((w >> 8) + 0.5) / 2^24.  Near U = 1 (where the largest Gumbel values
+// come from) E is computed from t = 1 - U, which is exact in fp32, by the
+// series -ln(1 - t) = t + t^2/2 + t^3/3 (t < 2^-10: truncation < t^4/4).
+__device__ __forceinline__ float gumbel2(uint32_t w) {
+  const uint32_t k = w >> 8;
+  const float u = ((float)k + 0.5f) * (1.0f / 16777216.0f);
+  const float t = ((float)(16777216u - k) - 0.5f) * (1.0f / 16777216.0f);
+  const float e_series = t * fmaf(t, fmaf(t, 1.0f / 3.0f, 0.5f), 1.0f) * kLog2e;
+  const float e_log = -__builtin_amdgcn_logf(u);  // -log2 U = E log2 e
+  return -__builtin_amdgcn_logf(t < (1.0f / 1024.0f) ? e_series : e_log);
+}
+
+struct RowState {
+  float m2, s;     // running max and sum of exp2(xs - m2)
+  float best;      // best Gumbel score
+  int32_t best_i;  // its vocabulary index
+};
+
+__device__ __forceinline__ void take(RowState& st, float score, int32_t i) {
+  if (score > st.best) {  // elements arrive in increasing index per lane
+    st.best = score;
+    st.best_i = i;
+  }
+}
+
+__device__ __forceinline__ void merge(RowState& a, const RowState& b) {
+  const float mn = fmaxf(a.m2, b.m2);
+  a.s = a.s * fast_exp2(a.m2 - mn) + b.s * fast_exp2(b.m2 - mn);
+  a.m2 = mn;
+  if (b.best > a.best || (b.best == a.best && b.best_i < a.best_i)) {
+    a.best = b.best;
+    a.best_i = b.best_i;
+  }
+}
+
+__device__ __forceinline__ RowState shfl_state(const RowState& st, int mask) {
+  RowState o;
+  o.m2 = __shfl_xor(st.m2, mask, 64);
+  o.s = __shfl_xor(st.s, mask, 64);
+  o.best = __shfl_xor(st.best, mask, 64);
+  o.best_i = __shfl_xor(st.best_i, mask, 64);
+  return o;
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void sample_rows(
+    const uint16_t* __restrict__ logits, int64_t row_stride, int64_t vocab, float c2,
+    uint32_t seed_lo, uint32_t seed_hi, uint32_t off_lo, uint32_t off_hi,
+    int64_t* __restrict__ out_tok, float* __restrict__ out_lp) {
+  __shared__ RowState sm[kWaves];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const uint16_t* rp = logits + row * row_stride;
+  const uint32_t crow = (uint32_t)row;
+  RowState st{kNegBig, 0.f, -INFINITY, 0};
+
+  int64_t tail_begin = 0;
+  if (VEC) {
+    const int64_t nvec = vocab >> 3;
+    tail_begin = nvec << 3;
+    for (int64_t i = tid; i < nvec; i += kThreads) {
+      const uint4 c = load_u4_stream(rp + (i << 3));
+      float xs[8];
+      xs[0] = bf16_lo(c.x) * c2; xs[1] = bf16_hi(c.x) * c2;
+      xs[2] = bf16_lo(c.y) * c2; xs[3] = bf16_hi(c.y) * c2;
+      xs[4] = bf16_lo(c.z) * c2; xs[5] = bf16_hi(c.z) * c2;
+      xs[6] = bf16_lo(c.w) * c2; xs[7] = bf16_hi(c.w) * c2;
+      const uint4 r0 = philox4x32_10(make_uint4((uint32_t)(2 * i), crow, off_lo, off_hi), seed_lo, seed_hi);
+      const uint4 r1 = philox4x32_10(make_uint4((uint32_t)(2 * i + 1), crow, off_lo, off_hi), seed_lo, seed_hi);
+      const uint32_t w[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+      float cm = xs[0];
+#pragma unroll
+      for (int e = 1; e < 8; ++e) cm = fmaxf(cm, xs[e]);
+      const float mn = fmaxf(st.m2, cm);
+      float add = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) add += fast_exp2(xs[e] - mn);
+      st.s = st.s * fast_exp2(st.m2 - mn) + add;
+      st.m2 = mn;
+      const int32_t e0 = (int32_t)(i << 3);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) take(st, xs[e] + gumbel2(w[e]), e0 + e);
+    }
+  }
+  // Scalar elements: the whole row when rows are not 16-byte aligned, else the tail.
+  for (int64_t e = tail_begin + tid; e < vocab; e += kThreads) {
+    const float xs = bf16_to_f32(rp[e]) * c2;
+    const uint4 r = philox4x32_10(make_uint4((uint32_t)(e >> 2), crow, off_lo, off_hi), seed_lo, seed_hi);
+    const int k = (int)(e & 3);
+    const uint32_t w = k == 0 ? r.x : k == 1 ? r.y : k == 2 ? r.z : r.w;
+    const float mn = fmaxf(st.m2, xs);
+    st.s = st.s * fast_exp2(st.m2 - mn) + fast_exp2(xs - mn);
+    st.m2 = mn;
+    take(st, xs + gumbel2(w), (int32_t)e);
+  }
+
+  // Workgroup reduction: within each wave by shuffles, then across waves.
+#pragma unroll
+  for (int mask = 32; mask >= 1; mask >>= 1) merge(st, shfl_state(st, mask));
+  if ((tid & 63) == 0) sm[tid >> 6] = st;
+  __syncthreads();
+  if (tid == 0) {
+    RowState a = sm[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) merge(a, sm[w]);
+    const int32_t tok = a.best_i;
+    out_tok[row] = tok;
+    if (out_lp) {
+      const float lse2 = a.m2 + __builtin_amdgcn_logf(a.s);
+      out_lp[row] = (bf16_to_f32(rp[tok]) * c2 - lse2) * kLn2;
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" int qmi_sample_tokens(const uint16_t* logits, int64_t row_stride, int64_t n_rows,
+                                 int64_t vocab, float temperature, uint64_t seed,
+                                 uint64_t offset, int64_t* out_tokens, float* out_logprobs,
+                                 void* stream) {
+  if (n_rows < 0 || vocab < 0) return QMI_E_BAD_SHAPE;
+  if (n_rows == 0) return QMI_OK;
+  if (!logits || !out_tokens) return QMI_E_NULL_POINTER;
+  if (vocab == 0 || vocab > 0x7fffffff) return QMI_E_BAD_SHAPE;
+  if (row_stride < vocab) return QMI_E_BAD_STRIDE;
+  if (n_rows > 0x7fffffff) return QMI_E_UNSUPPORTED;
+  if (!(temperature > 0.f) || temperature == INFINITY) return QMI_E_BAD_SHAPE;
+  const float c2 = kLog2e / temperature;
+  const uint32_t s_lo = (uint32_t)seed, s_hi = (uint32_t)(seed >> 32);
+  const uint32_t o_lo = (uint32_t)offset, o_hi = (uint32_t)(offset >> 32);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const bool vec = (row_stride % 8 == 0) && ((reinterpret_cast<uintptr_t>(logits) & 15u) == 0);
+  if (vec)
+    hipLaunchKernelGGL(sample_rows<true>, dim3((unsigned)n_rows), dim3(kThreads), 0, s, logits,
+                       row_stride, vocab, c2, s_lo, s_hi, o_lo, o_hi, out_tokens, out_logprobs);
+  else
+    hipLaunchKernelGGL(sample_rows<false>, dim3((unsigned)n_rows), dim3(kThreads), 0, s, logits,
+                       row_stride, vocab, c2, s_lo, s_hi, o_lo, o_hi, out_tokens, out_logprobs);
+  QMI_RETURN_LAUNCH_STATUS();
+}

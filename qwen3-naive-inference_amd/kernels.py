@@ -342,6 +342,35 @@ def logprob_gather(logits: torch.Tensor, ids: torch.Tensor, need_lse: bool = Tru
     return lp.view(shape), (lse.view(shape) if lse is not None else None)
 
 
+def sample_tokens(logits: torch.Tensor, temperature: float = 1.0, seed: int | None = None,
+                  offset: int = 0, want_logprobs: bool = True):
+    """Draw one token per row from ``softmax(logits.float() / temperature)`` and
+    return ``(tokens int64 [N], log_softmax(...)[token] fp32 [N] or None)``.
+
+    ``logits``: ``[N, V]`` bf16 with unit vocab stride.  ``seed`` defaults to a
+    draw from torch's default CPU generator, so ``torch.manual_seed`` makes
+    the tokens reproducible; the same ``(seed, offset)`` gives the same tokens.
+    """
+    _require_cuda("logits", logits)
+    _require_dtype("logits", logits, torch.bfloat16)
+    if logits.dim() != 2:
+        raise ValueError(f"logits must be [N, V], got {tuple(logits.shape)}")
+    if not (temperature > 0.0) or temperature == float("inf"):
+        raise ValueError(f"temperature must be finite and > 0, got {temperature}")
+    if logits.stride(1) != 1:
+        logits = logits.contiguous()
+    n, v = logits.shape
+    if seed is None:
+        seed = int(torch.randint(0, 2 ** 62, (1,)).item())
+    tok = torch.empty((n,), dtype=torch.int64, device=logits.device)
+    lp = torch.empty((n,), dtype=torch.float32, device=logits.device) if want_logprobs else None
+    st = lib().qmi_sample_tokens(logits.data_ptr(), logits.stride(0), n, v, float(temperature),
+                                 int(seed) & (2 ** 64 - 1), int(offset) & (2 ** 64 - 1),
+                                 tok.data_ptr(), _ptr(lp), stream_handle(logits.device))
+    check(st, "sample_tokens")
+    return tok, lp
+
+
 def logprob_gather_backward(logits: torch.Tensor, ids: torch.Tensor, lse: torch.Tensor,
                             coef: torch.Tensor, grad_scale: torch.Tensor | None = None,
                             out: torch.Tensor | None = None) -> torch.Tensor:

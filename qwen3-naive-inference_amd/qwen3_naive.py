@@ -545,7 +545,13 @@ class Qwen3ForCausalLM(nn.Module):
 
     def _sample(self, logits, temperature, top_k, want_logprobs):
         """Temperature / top-k / softmax / multinomial (qwen3_naive.py:1413-1423) and,
-        optionally, the sampled tokens' log-probabilities (:1649-1650)."""
+        optionally, the sampled tokens' log-probabilities (:1649-1650).
+
+        Without top-k the fused HIP sampler draws the tokens (Gumbel-max over
+        Philox uniforms, seeded from torch's CPU generator) and returns their
+        log-probabilities in the same pass over the bf16 logits."""
+        if top_k is None and logits.dtype == torch.bfloat16:
+            return K.sample_tokens(logits, temperature, want_logprobs=want_logprobs)
         x = logits.float()
         if temperature != 1.0:
             x = x / temperature
@@ -553,12 +559,7 @@ class Qwen3ForCausalLM(nn.Module):
             vals, idx = torch.topk(x, top_k, dim=-1)
             x = torch.full_like(x, float("-inf")).scatter(-1, idx, vals)
         nxt = torch.multinomial(torch.softmax(x, dim=-1), num_samples=1)
-        lp = None
-        if want_logprobs:
-            if temperature == 1.0 and top_k is None and logits.dtype == torch.bfloat16:
-                lp, _ = K.logprob_gather(logits.contiguous(), nxt[:, 0], need_lse=False)
-            else:
-                lp = torch.log_softmax(x, dim=-1).gather(-1, nxt)[:, 0]
+        lp = torch.log_softmax(x, dim=-1).gather(-1, nxt)[:, 0] if want_logprobs else None
         return nxt[:, 0], lp
 
     @torch.no_grad()

@@ -1,0 +1,52 @@
+"""Sampling oracle: Philox4x32-10 against its authors' known-answer vectors,
+the uniform mapping, and the Gumbel-max draw against softmax frequencies."""
+import numpy as np
+import torch
+from scipy import stats
+
+from oracle import sampling as OS
+
+
+def test_philox_known_answers():
+    # Known-answer vectors of Philox4x32-10 published with the Random123
+    # library (counter, key) -> output.
+    cases = [
+        ((0, 0, 0, 0), (0, 0), (0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8)),
+        ((0xFFFFFFFF,) * 4, (0xFFFFFFFF, 0xFFFFFFFF), (0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD)),
+        ((0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344), (0xA4093822, 0x299F31D0),
+         (0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1)),
+    ]
+    for ctr, key, want in cases:
+        got = OS.philox4x32_10(np.array([ctr], dtype=np.uint32), key)[0]
+        assert tuple(int(x) for x in got) == want
+
+
+def test_uniforms_open_interval_and_layout():
+    u = OS.uniforms(3, 11, seed=5, offset=7)
+    assert u.shape == (3, 11) and (u > 0).all() and (u < 1).all()
+    # element i of row r is word i % 4 of block (i // 4, r, offset)
+    w = OS.philox4x32_10(np.array([[2, 1, 7, 0]], dtype=np.uint32), (5, 0))[0]
+    assert u[1, 9] == ((int(w[1]) >> 8) + 0.5) / 2 ** 24
+
+
+def test_gumbel_max_matches_softmax_frequencies():
+    logits = torch.tensor([[2.0, 1.0, 0.5, 0.0, -1.0, 3.0]]).to(torch.bfloat16)
+    for temp in (1.0, 0.7):
+        n = 40000
+        sc = OS.gumbel_scores(logits.expand(n, -1).contiguous(), temp, seed=11, offset=3)
+        counts = np.bincount(sc.argmax(-1), minlength=6)
+        p = OS.probs(logits, temp)[0].numpy()
+        chi2 = ((counts - n * p) ** 2 / (n * p)).sum()
+        assert chi2 < stats.chi2.ppf(0.999, df=5), (temp, chi2, counts, n * p)
+
+
+def test_logprob_of_is_log_softmax():
+    g = torch.Generator().manual_seed(0)
+    logits = (3 * torch.randn(4, 50, generator=g)).to(torch.bfloat16)
+    tok = torch.tensor([0, 7, 49, 3])
+    lp = OS.logprob_of(logits, tok, 0.8)
+    x = logits.double() / 0.8
+    want = x.gather(-1, tok[:, None])[:, 0] - torch.logsumexp(x, -1)
+    assert torch.allclose(lp, want, atol=1e-12)
+    # probabilities of a row sum to one
+    assert torch.allclose(OS.probs(logits, 0.8).sum(-1), torch.ones(4, dtype=torch.float64))
