@@ -168,6 +168,24 @@ int qmi_qk_norm_rope(const uint16_t* qkv, int64_t qkv_stride, int64_t n_tok, int
                      void* stream);
 
 /*
+ * qmi_qk_norm_rope with the KV store fused in: q goes to q_out as above; the
+ * rotated k head and the token's v head (the last Hkv heads of the qkv row,
+ * unchanged) go to row slot_mapping[tok] of k_cache / v_cache ([n_slots,
+ * Hkv * 128] bf16 rows, i.e. [num_blocks * 256] slots of the paged pool);
+ * slots outside [0, n_slots) are skipped.  Replaces q_norm / k_norm + RoPE +
+ * store_kvcache(k, v, ...) in Qwen3Attention.forward_prefill
+ * (qwen3_naive.py:611-626) and forward_decode (:655-668); results are
+ * bit-identical to qmi_qk_norm_rope followed by qmi_store_kvcache.
+ */
+int qmi_qk_norm_rope_store(const uint16_t* qkv, int64_t qkv_stride, int64_t n_tok,
+                           int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                           const uint16_t* q_norm_weight, const uint16_t* k_norm_weight,
+                           const int64_t* positions, const float* cos_sin_cache,
+                           int64_t max_position, uint16_t* q_out, int64_t q_stride,
+                           uint16_t* k_cache, uint16_t* v_cache, const int32_t* slot_mapping,
+                           int64_t n_slots, float eps, void* stream);
+
+/*
  * SwiGLU activation of the fused gate_up projection.  Replaces
  * `silu(gate) * up` of Qwen3MLP.forward (qwen3_naive.py:695-702):
  * out[r, j] = bf16(silu(g) * u) with g = gate_up[r, j], u = gate_up[r, inter + j].

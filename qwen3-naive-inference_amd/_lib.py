@@ -51,6 +51,9 @@ SIGNATURES: dict[str, tuple] = {
     "qmi_qk_norm_rope": (ctypes.c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p,
                                         _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_i64, _c_f32,
                                         _c_p]),
+    "qmi_qk_norm_rope_store": (ctypes.c_int, [
+        _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_p,
+        _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_f32, _c_p]),
     "qmi_silu_mul": (ctypes.c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p]),
     "qmi_logprob_gather": (ctypes.c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i64,
                                           _c_i64, _c_i64, _c_p, _c_p, _c_p]),

@@ -94,12 +94,17 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_rows(
 // ---------------------------------------------------------------------------
 // Fused per-head RMSNorm + RoPE for q and k of a fused qkv row.
 // One wave64 per (token, head); lane j < 64 owns the RoPE pair (j, j + 64).
+// k goes to k_out (when given) and, with the caches given, the rotated k and
+// the token's v head go straight to cache row slots[tok] (slots outside
+// [0, n_slots) are skipped, as in the KV store).
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     const uint16_t* __restrict__ qkv, int64_t qkv_stride, int n_q_heads, int n_kv_heads,
     const uint16_t* __restrict__ q_w, const uint16_t* __restrict__ k_w,
     const int64_t* __restrict__ positions, const float* __restrict__ cos_sin,
     int64_t max_pos, uint16_t* __restrict__ q_out, int64_t q_stride,
-    uint16_t* __restrict__ k_out, int64_t k_stride, int64_t n_tok, float eps) {
+    uint16_t* __restrict__ k_out, int64_t k_stride, uint16_t* __restrict__ k_cache,
+    uint16_t* __restrict__ v_cache, const int32_t* __restrict__ slots, int64_t n_slots,
+    int64_t n_tok, float eps) {
   constexpr int D = 128, HALF = 64;
   const int lane = threadIdx.x & 63;
   const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -123,10 +128,30 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
   const float s = cos_sin[pos * D + HALF + lane];
   const float o1 = n1 * c - n2 * s;
   const float o2 = n2 * c + n1 * s;
-  uint16_t* dst = is_q ? q_out + tok * q_stride + (int64_t)h * D
-                       : k_out + tok * k_stride + (int64_t)(h - n_q_heads) * D;
-  dst[lane] = f32_to_bf16(o1);
-  dst[lane + HALF] = f32_to_bf16(o2);
+  const uint16_t b1 = f32_to_bf16(o1), b2 = f32_to_bf16(o2);
+  if (is_q) {
+    uint16_t* dst = q_out + tok * q_stride + (int64_t)h * D;
+    dst[lane] = b1;
+    dst[lane + HALF] = b2;
+    return;
+  }
+  const int hk = h - n_q_heads;
+  if (k_out) {
+    uint16_t* dst = k_out + tok * k_stride + (int64_t)hk * D;
+    dst[lane] = b1;
+    dst[lane + HALF] = b2;
+  }
+  if (k_cache) {
+    const int64_t slot = slots[tok];
+    if (slot >= 0 && slot < n_slots) {
+      const int64_t row = slot * n_kv_heads * D + (int64_t)hk * D;
+      k_cache[row + lane] = b1;
+      k_cache[row + lane + HALF] = b2;
+      const uint16_t* vsrc = qkv + tok * qkv_stride + (int64_t)(n_q_heads + n_kv_heads + hk) * D;
+      v_cache[row + lane] = vsrc[lane];
+      v_cache[row + lane + HALF] = vsrc[lane + HALF];
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -213,7 +238,34 @@ extern "C" int qmi_qk_norm_rope(const uint16_t* qkv, int64_t qkv_stride, int64_t
   hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0,
                      reinterpret_cast<hipStream_t>(stream), qkv, qkv_stride, (int)num_q_heads,
                      (int)num_kv_heads, q_norm_weight, k_norm_weight, positions, cos_sin_cache,
-                     max_position, q_out, q_stride, k_out, k_stride, n_tok, eps);
+                     max_position, q_out, q_stride, k_out, k_stride, nullptr, nullptr, nullptr,
+                     (int64_t)0, n_tok, eps);
+  QMI_RETURN_LAUNCH_STATUS();
+}
+
+extern "C" int qmi_qk_norm_rope_store(
+    const uint16_t* qkv, int64_t qkv_stride, int64_t n_tok, int64_t num_q_heads,
+    int64_t num_kv_heads, int64_t head_dim, const uint16_t* q_norm_weight,
+    const uint16_t* k_norm_weight, const int64_t* positions, const float* cos_sin_cache,
+    int64_t max_position, uint16_t* q_out, int64_t q_stride, uint16_t* k_cache,
+    uint16_t* v_cache, const int32_t* slot_mapping, int64_t n_slots, float eps, void* stream) {
+  if (n_tok < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || max_position <= 0 || n_slots < 0)
+    return QMI_E_BAD_SHAPE;
+  if (n_tok == 0) return QMI_OK;
+  if (!qkv || !q_norm_weight || !k_norm_weight || !positions || !cos_sin_cache || !q_out ||
+      !k_cache || !v_cache || !slot_mapping)
+    return QMI_E_NULL_POINTER;
+  if (head_dim != 128) return QMI_E_UNSUPPORTED;
+  if (num_q_heads > 4096 || num_kv_heads > 4096) return QMI_E_UNSUPPORTED;
+  if (qkv_stride < (num_q_heads + 2 * num_kv_heads) * head_dim || q_stride < num_q_heads * 128)
+    return QMI_E_BAD_STRIDE;
+  const int64_t items = n_tok * (num_q_heads + num_kv_heads);
+  if ((items + 3) / 4 > 0x7fffffffLL) return QMI_E_UNSUPPORTED;
+  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), qkv, qkv_stride, (int)num_q_heads,
+                     (int)num_kv_heads, q_norm_weight, k_norm_weight, positions, cos_sin_cache,
+                     max_position, q_out, q_stride, nullptr, (int64_t)0, k_cache, v_cache,
+                     slot_mapping, n_slots, n_tok, eps);
   QMI_RETURN_LAUNCH_STATUS();
 }
 

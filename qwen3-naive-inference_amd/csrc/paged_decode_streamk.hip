@@ -124,6 +124,10 @@ void decode_streamk_split(
   const uint32_t lane_off = (uint32_t)(tg * kTok * kRowBytes + (h * kHeadDim + lane16 * 8) * 2);
 
   scan_steps<kThreads, TS>(seqlens, seqlen_bias, bt_width, batch, off);
+  if (w == 0) {  // publish the step offsets for the merge kernel
+    int32_t* ws_off = reinterpret_cast<int32_t*>(ws + (int64_t)n_wg * 2 * HQ * kSlotStride);
+    for (int i = tid; i <= batch; i += kThreads) ws_off[i] = off[i];
+  }
   const int64_t total = off[batch];
   if (total == 0) return;
   const int64_t s_begin = range_start(w, total, n_wg);
@@ -300,26 +304,25 @@ void decode_streamk_split(
 }
 
 // Combines the partial slots of sequences shared by several workgroups and
-// writes zeros for empty sequences.  One workgroup per (sequence, query head):
-// 16 groups of 16 lanes take every 16th sharing workgroup (a lane owns 8
-// output dims), so the slot loads of up to 16 workgroups are in flight at
-// once; the 16 group states are then combined through LDS.
+// writes zeros for empty sequences, reading the step offsets the split kernel
+// published after its slots.  One workgroup per (sequence, query head): 16
+// groups of 16 lanes take every 16th sharing workgroup (a lane owns 8 output
+// dims), so up to 16 slots are read at once; the group states are combined
+// through LDS.
 template <int HKV, int G>
 __global__ __launch_bounds__(kThreads) void decode_streamk_merge(
-    const int32_t* __restrict__ seqlens, int seqlen_bias, int bt_width, int batch, int n_wg,
-    const float* __restrict__ ws, uint16_t* __restrict__ out, int64_t out_seq_stride,
-    int64_t out_head_stride) {
+    int batch, int n_wg, const float* __restrict__ ws, uint16_t* __restrict__ out,
+    int64_t out_seq_stride, int64_t out_head_stride) {
   constexpr int HQ = HKV * G;
   constexpr int kGroups = kThreads / 16;
-  __shared__ int off[kMaxSeqScan + 1];
   __shared__ float s_ml[kGroups][2];
   __shared__ float s_acc[kGroups][kHeadDim];
-  scan_steps<kThreads, kStepTokens<HKV>>(seqlens, seqlen_bias, bt_width, batch, off);
+  const int32_t* ws_off = reinterpret_cast<const int32_t*>(ws + (int64_t)n_wg * 2 * HQ * kSlotStride);
   const int b = blockIdx.x, qh = blockIdx.y;
   const int tid = threadIdx.x, lane16 = tid & 15, grp = tid >> 4;
   uint16_t* o_row = out + (int64_t)b * out_seq_stride + (int64_t)qh * out_head_stride;
-  const int64_t total = off[batch];
-  const int64_t sb = off[b], se = off[b + 1];
+  const int64_t total = ws_off[batch];
+  const int64_t sb = ws_off[b], se = ws_off[b + 1];
   if (se == sb) {  // empty sequence attends to nothing: zeros, as flash-attn
     if (tid < kHeadDim) o_row[tid] = 0;
     return;
@@ -402,7 +405,10 @@ int64_t streamk_workgroups(int64_t batch, int64_t num_q_heads, int64_t num_kv_he
 
 int64_t streamk_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
                                 int64_t bt_width) {
-  return streamk_workgroups(batch, num_q_heads, num_kv_heads, bt_width) * 2 * num_q_heads * kSlotStride * (int64_t)sizeof(float);
+  // partial slots, then the published step offsets (int32 [batch + 1])
+  return streamk_workgroups(batch, num_q_heads, num_kv_heads, bt_width) * 2 * num_q_heads *
+             kSlotStride * (int64_t)sizeof(float) +
+         (batch + 1) * (int64_t)sizeof(int32_t);
 }
 
 bool streamk_supported(int64_t num_q_heads, int64_t num_kv_heads, int64_t batch) {
@@ -424,8 +430,7 @@ static int launch(const uint16_t* q, int64_t qs, int64_t qh, const uint16_t* kc,
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
   hipLaunchKernelGGL((decode_streamk_merge<HKV, G>), dim3((unsigned)batch, (unsigned)(HKV * G)),
-                     dim3(kThreads), 0, s,
-                     lens, (int)bias, (int)btw, (int)batch, (int)n_wg, ws, out, os, oh);
+                     dim3(kThreads), 0, s, (int)batch, (int)n_wg, ws, out, os, oh);
   QMI_RETURN_LAUNCH_STATUS();
 }
 

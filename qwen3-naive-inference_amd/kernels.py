@@ -291,6 +291,52 @@ def qk_norm_rope(qkv: torch.Tensor, q_norm_weight: torch.Tensor, k_norm_weight: 
     return q, k
 
 
+def qk_norm_rope_store(qkv: torch.Tensor, q_norm_weight: torch.Tensor,
+                       k_norm_weight: torch.Tensor, positions: torch.Tensor,
+                       cos_sin_cache: torch.Tensor, num_q_heads: int, num_kv_heads: int,
+                       eps: float, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                       slot_mapping: torch.Tensor) -> torch.Tensor:
+    """``qk_norm_rope`` with the KV store fused in: returns ``q [N, Hq, 128]`` and
+    writes the rotated k and the v heads of ``qkv`` to cache rows ``slot_mapping``
+    (-1 skips), bit-identical to ``qk_norm_rope`` + ``store_kvcache``."""
+    _require_cuda("qkv", qkv)
+    _require_dtype("qkv", qkv, torch.bfloat16)
+    if qkv.dim() != 2 or qkv.stride(1) != 1:
+        raise ValueError("qkv must be a row-major [N, (Hq + 2 Hkv) * 128] tensor")
+    n = qkv.shape[0]
+    pos = positions.reshape(-1)
+    if pos.dtype != torch.int64:
+        pos = pos.to(torch.int64)
+    if pos.shape[0] != n:
+        raise ValueError(f"positions must have {n} entries")
+    pos = pos.contiguous()
+    cache = cos_sin_cache
+    if cache.dtype != torch.float32 or cache.dim() != 2 or cache.shape[1] != HEAD_DIM:
+        raise ValueError("cos_sin_cache must be fp32 [max_position, 128]")
+    cache = cache.contiguous()
+    for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
+        _require_cuda(name, c)
+        _require_dtype(name, c, torch.bfloat16)
+        if not c.is_contiguous() or c.shape[-2:] != (num_kv_heads, HEAD_DIM):
+            raise ValueError(f"{name} must be a contiguous [..., {num_kv_heads}, 128] bf16 pool")
+    sl = slot_mapping.reshape(-1)
+    if sl.dtype != torch.int32:
+        sl = sl.to(torch.int32)
+    if sl.shape[0] != n:
+        raise ValueError(f"slot_mapping must have {n} entries")
+    sl = sl.contiguous()
+    n_slots = k_cache.numel() // (num_kv_heads * HEAD_DIM)
+    qw = q_norm_weight.to(torch.bfloat16).contiguous()
+    kw = k_norm_weight.to(torch.bfloat16).contiguous()
+    q = torch.empty((n, num_q_heads, HEAD_DIM), dtype=torch.bfloat16, device=qkv.device)
+    check(lib().qmi_qk_norm_rope_store(
+        qkv.data_ptr(), qkv.stride(0), n, num_q_heads, num_kv_heads, HEAD_DIM, qw.data_ptr(),
+        kw.data_ptr(), pos.data_ptr(), cache.data_ptr(), cache.shape[0], q.data_ptr(),
+        q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(), sl.data_ptr(), n_slots, float(eps),
+        stream_handle(qkv.device)), "qk_norm_rope_store")
+    return q
+
+
 def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
     """``silu(gate) * up`` of a fused ``[..., 2 * inter]`` projection (one bf16 rounding)."""
     g2 = _rows2d("gate_up", gate_up)

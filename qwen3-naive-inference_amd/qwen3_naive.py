@@ -175,6 +175,14 @@ class Qwen3Attention(nn.Module):
         v = qkv[:, self.q_size + self.kv_size:].view(x.shape[0], self.num_kv_heads, self.head_dim)
         return q, k, v
 
+    def _project_store(self, x, positions, slots):
+        """qkv projection + fused QK-norm/RoPE/KV-store kernel -> q [N,Hq,D]; the
+        rotated k and v land in the cache rows ``slots``."""
+        qkv = self.qkv_proj(x)
+        return K.qk_norm_rope_store(qkv, self.q_norm.weight, self.k_norm.weight, positions,
+                                    self._cos_sin(x.device), self.num_heads, self.num_kv_heads,
+                                    self.eps, self.k_cache, self.v_cache, slots)
+
     # ----- batch path (training / no-cache eager forward, qwen3_naive.py:553-593) -----
     def forward(self, x):
         batch, seq_len, _ = x.shape
@@ -207,8 +215,7 @@ class Qwen3Attention(nn.Module):
         """Varlen prefill/mixed step: store the new K/V through ``block_mapping``,
         then attend over the paged cache (prefix + earlier chunks + this chunk)."""
         tokens = x.shape[0]
-        q, k, v = self._project(x, positions)
-        store_kvcache(k, v, self.k_cache, self.v_cache, block_mapping)
+        q = self._project_store(x, positions, block_mapping)
         o = K.varlen_prefill_attention(q, self.k_cache, self.v_cache, cu_seqlens_q, cu_seqlens_k,
                                        max_seqlen_q, max_seqlen_k, self.scale, True, block_tables)
         return self.o_proj(o.view(tokens, -1))
@@ -217,12 +224,11 @@ class Qwen3Attention(nn.Module):
         """One new token per sequence: store its K/V at ``slot_mapping`` (derived
         from the tables when None) and attend over ``context_lens + 1`` keys."""
         batch = x.shape[0]
-        q, k, v = self._project(x, positions)
         if slot_mapping is None:
             ctx = context_lens.long()
             blk = block_tables.long().gather(1, (ctx // BLOCK_SIZE)[:, None])[:, 0]
             slot_mapping = (blk * BLOCK_SIZE + ctx % BLOCK_SIZE).to(torch.int32)
-        store_kvcache(k, v, self.k_cache, self.v_cache, slot_mapping)
+        q = self._project_store(x, positions, slot_mapping)
         o = K.paged_decode_attention(q, self.k_cache, self.v_cache, context_lens, block_tables,
                                      self.scale, seqlen_bias=1)
         return self.o_proj(o.view(batch, -1))

@@ -67,6 +67,33 @@ def test_qk_norm_rope(pkg, gpu):
     assert torch.equal(q[0].cpu(), qn[0])        # position 0 rotates by identity
 
 
+def test_qk_norm_rope_store_equals_separate_kernels(pkg, gpu):
+    """The fused store writes exactly what qk_norm_rope + store_kvcache write
+    (bit-identical q, K and V rows); slots -1 and past the pool are skipped."""
+    g = torch.Generator().manual_seed(3)
+    n, hq, hkv, nb = 40, 16, 8, 3
+    qkv = (torch.randn(n, (hq + 2 * hkv) * 128, generator=g) * 2).to(torch.bfloat16).to(gpu)
+    qw = (torch.rand(128, generator=g) + 0.5).to(torch.bfloat16).to(gpu)
+    kw = (torch.rand(128, generator=g) + 0.5).to(torch.bfloat16).to(gpu)
+    pos = torch.randint(0, 4096, (n,), generator=g).to(gpu)
+    slots = torch.randperm(nb * 256, generator=g)[:n].to(torch.int32)
+    slots[3], slots[7] = -1, nb * 256 + 5
+    slots = slots.to(gpu)
+    cache = NR.rope_cache(128, 40960, 1e6).to(gpu)
+    base_k = torch.randn(nb, 256, hkv, 128, generator=g).to(torch.bfloat16).to(gpu)
+    base_v = torch.randn(nb, 256, hkv, 128, generator=g).to(torch.bfloat16).to(gpu)
+    print("[norm] qk norm + rope + store", flush=True)
+    k1, v1 = base_k.clone(), base_v.clone()
+    q1, kk = pkg.kernels.qk_norm_rope(qkv, qw, kw, pos, cache, hq, hkv, 1e-6)
+    vv = qkv[:, (hq + hkv) * 128:].view(n, hkv, 128)
+    pkg.kernels.store_kvcache(kk, vv, k1, v1, slots)
+    k2, v2 = base_k.clone(), base_v.clone()
+    q2 = pkg.kernels.qk_norm_rope_store(qkv, qw, kw, pos, cache, hq, hkv, 1e-6, k2, v2, slots)
+    torch.cuda.synchronize()
+    assert torch.equal(q1, q2) and torch.equal(k1, k2) and torch.equal(v1, v2)
+    assert not torch.equal(k2, base_k)
+
+
 def test_silu_mul(pkg, gpu):
     g = torch.Generator().manual_seed(3)
     gu = (torch.randn(33, 2 * 3072, generator=g) * 2).to(torch.bfloat16)
