@@ -323,6 +323,8 @@ class Qwen3Model(nn.Module):
 # runs larger batches eagerly; the 288 GB HBM affords buckets up to 256.
 GRAPH_BATCH_SIZES = (1, 2, 4, 8, 16, 32, 48, 64, 96, 128, 160, 192, 256)
 MAX_TOKENS_PER_STEP = 2048
+# Stands in for a sampled token whose value is still on the device (decode lookahead).
+_PENDING_TOKEN = -1
 
 
 class Qwen3ForCausalLM(nn.Module):
@@ -346,6 +348,8 @@ class Qwen3ForCausalLM(nn.Module):
         self._graph_bufs = None
         self._graph_pool = None
         self._has_cuda_graphs = False
+        # Launch decode step t+1 before reading step t's tokens back (EOS-free runs).
+        self.decode_lookahead = True
 
     def forward(self, x):
         return self.lm_head(self.model(x))
@@ -583,13 +587,88 @@ class Qwen3ForCausalLM(nn.Module):
         all_seqs = list(waiting)
         running: list[Sequence] = []
         self._preemptions = 0
-        self.last_stats = {"steps": 0, "decode_steps": 0, "graph_steps": 0}
+        self.last_stats = {"steps": 0, "decode_steps": 0, "graph_steps": 0, "lookahead_steps": 0}
+        dev = self._device()
+        # Decode lookahead: without EOS a sequence finishes by count alone, so
+        # the host can launch decode step t+1 (its input ids gathered on the
+        # device from step t's samples) before it reads step t's tokens back;
+        # step t's tokens then fill placeholders while step t+1 runs.
+        lookahead = eos is None and self.decode_lookahead
+        pending = None
+
+        def flush():
+            nonlocal pending
+            if pending is None:
+                return
+            pending["event"].synchronize()
+            toks = pending["tok_host"].tolist()
+            lps = pending["lp_host"].tolist() if pending["lp_host"] is not None else None
+            for j, (s, at) in enumerate(pending["seqs"]):
+                if at >= len(s.token_ids) or s.token_ids[at] != _PENDING_TOKEN:
+                    continue  # preempted since (its tokens were rolled back)
+                s.token_ids[at] = toks[j]
+                if at == len(s.token_ids) - 1:
+                    s.last_token = toks[j]
+                if lps is not None:
+                    s.response_log_probs.append(lps[j])
+            pending = None
+
         while waiting or running:
             scheduled = self._schedule(waiting, running, bm)
             if not scheduled:
                 continue
             all_decode = all(s.num_scheduled_tokens == 1 for s in scheduled)
             self.last_stats["steps"] += 1
+            if all_decode and lookahead:
+                ids_dev = None
+                if pending is not None:
+                    rows = pending["row_of"]
+                    idx = [rows.get(id(s), -1) for s in scheduled]
+                    if min(idx) < 0:
+                        flush()
+                    elif idx == list(range(pending["n"])):
+                        ids_dev = pending["tok_dev"]
+                    else:
+                        ids_dev = pending["tok_dev"][torch.tensor(idx, device=dev)]
+                self.last_stats["decode_steps"] += 1
+                ids, pos, ctx, bt, slots = self._prepare_decode(scheduled)
+                if ids_dev is not None:
+                    ids = ids_dev
+                    self.last_stats["lookahead_steps"] += 1
+                h = None
+                if use_graphs and self._has_cuda_graphs:
+                    h = self._run_decode_graph(len(scheduled), ids, pos, ctx, bt, slots)
+                    if h is not None:
+                        self.last_stats["graph_steps"] += 1
+                if h is None:
+                    h = self.model.forward_decode(ids, pos, ctx, bt, slots)
+                nxt, lp = self._sample(self.lm_head(h), temperature, top_k, with_logprobs)
+                n = len(scheduled)
+                tok_host = torch.empty((n,), dtype=torch.int64, pin_memory=True)
+                tok_host.copy_(nxt, non_blocking=True)
+                lp_host = None
+                if lp is not None:
+                    lp_host = torch.empty((n,), dtype=torch.float32, pin_memory=True)
+                    lp_host.copy_(lp, non_blocking=True)
+                event = torch.cuda.Event()
+                event.record()
+                flush()  # the previous step's tokens, while this step runs
+                for s in scheduled:
+                    s.kv_len += 1
+                    s.append_token(_PENDING_TOKEN)
+                    s.num_scheduled_tokens = 0
+                pending = {"seqs": [(s, len(s.token_ids) - 1) for s in scheduled],
+                           "row_of": {id(s): j for j, s in enumerate(scheduled)}, "n": n,
+                           "tok_dev": nxt, "tok_host": tok_host, "lp_host": lp_host,
+                           "event": event}
+                for s in scheduled:
+                    if s.num_completion_tokens >= s.max_tokens:
+                        s.status = "FINISHED"
+                        bm.deallocate(s.block_table)
+                        s.block_table.clear()
+                        running.remove(s)
+                continue
+            flush()
             if all_decode:
                 self.last_stats["decode_steps"] += 1
                 ids, pos, ctx, bt, slots = self._prepare_decode(scheduled)
@@ -634,6 +713,7 @@ class Qwen3ForCausalLM(nn.Module):
                     running.remove(s)
             for s in scheduled:
                 s.num_scheduled_tokens = 0
+        flush()
         self.last_stats["preemptions"] = self._preemptions
         return all_seqs
 

@@ -211,3 +211,37 @@ def test_generation_with_preemption(pkg, model):
     finally:
         model._num_blocks = 0
         model.allocate_global_kv_cache(num_blocks=64)
+
+
+@pytest.mark.parametrize("graphs,blocks", [(True, None), (False, None), (True, 6)])
+def test_decode_lookahead_matches_synchronous_engine(pkg, model, graphs, blocks):
+    """Launching decode step t+1 before step t's tokens are read back changes
+    nothing: same tokens and log-probabilities as the synchronous engine, also
+    with a pool small enough to force LIFO preemption."""
+    g = torch.Generator().manual_seed(8)
+    # Four ~250-token prompts + 40 tokens need 8 pages at the end: 6 forces preemption.
+    prompts = [torch.randint(0, VOCAB, (1, n), generator=g) for n in (250, 240, 251, 245)]
+    if blocks is not None:
+        model.allocate_global_kv_cache(num_blocks=blocks)
+    try:
+        runs = []
+        for la in (False, True):
+            model.decode_lookahead = la
+            torch.manual_seed(3)
+            print(f"[model] lookahead={la} graphs={graphs} blocks={blocks}", flush=True)
+            out = model.generate_continuous_with_logprobs(prompts, max_new_tokens=40,
+                                                          temperature=1.0, top_k=None,
+                                                          use_graphs=graphs)
+            runs.append((out, dict(model.last_stats)))
+        (t0, _, l0, _), s0 = runs[0]
+        (t1, _, l1, _), s1 = runs[1]
+        assert t0 == t1 and l0 == l1
+        assert all(t >= 0 for seq in t1 for t in seq)
+        assert s1["lookahead_steps"] > 0 and s0["lookahead_steps"] == 0
+        if blocks is not None:
+            assert s1["preemptions"] > 0 and s1["preemptions"] == s0["preemptions"]
+    finally:
+        model.decode_lookahead = True
+        if blocks is not None:
+            model._num_blocks = 0
+            model.allocate_global_kv_cache(num_blocks=64)
