@@ -124,7 +124,22 @@ def leg_grpo(torch, pkg, W, dev, steps, warmup):
     torch.cuda.synchronize()
     out = dict(avg_launch_us=ms * 1e3, gbs=nbytes / (ms * 1e-3) / 1e9, bytes_per_launch=nbytes,
                loss=float(res["loss"].item()))
-    del w, args, res
+    # Backward through the log-softmax (d loss / d logits, bf16): rows with a
+    # non-zero coefficient read their logits, every row writes its gradient.
+    log("grpo: backward timing")
+    grad = torch.empty_like(w["logits"])
+    lse, dlp = res["lse"], res["dlp"]
+    gscale = torch.ones((), dtype=torch.float32, device=dev)
+    bwd = lambda: pkg.kernels.logprob_gather_backward(w["logits"], w["ids"], lse, dlp,
+                                                      grad_scale=gscale, out=grad)
+    _, per_b = timed_launches(torch, [bwd], max(3, steps // 2), warmup)
+    ms_b = statistics.mean(per_b)
+    active = int((dlp != 0).sum().item())
+    row_bytes = 151936 * 2
+    b_bytes = active * row_bytes + rows * row_bytes + rows * (8 + 8)
+    out.update(bwd_avg_launch_us=ms_b * 1e3, bwd_gbs=b_bytes / (ms_b * 1e-3) / 1e9,
+               bwd_bytes_per_launch=b_bytes, bwd_active_rows=active)
+    del w, args, res, grad
     torch.cuda.empty_cache()
     return out
 
@@ -517,6 +532,12 @@ def main() -> int:
             "frac_of_hbm_peak": round(r["gbs"] / HBM_PEAK_GBS, 4),
             "bytes_per_launch": r["bytes_per_launch"], "loss": r["loss"],
             "cpu_baseline": cpu_grpo}
+        secondary["grpo_logprob_backward"] = {
+            "workload": "d loss / d logits through log_softmax (bf16 out), same 32x512x151936 "
+                        "rows; masked rows only write zeros",
+            "us_per_launch": round(r["bwd_avg_launch_us"], 2), "gbs": round(r["bwd_gbs"], 1),
+            "frac_of_hbm_peak": round(r["bwd_gbs"] / HBM_PEAK_GBS, 4),
+            "bytes_per_launch": r["bwd_bytes_per_launch"], "active_rows": r["bwd_active_rows"]}
     if "store" in results:
         r = results["store"]
         secondary["kv_store"] = {

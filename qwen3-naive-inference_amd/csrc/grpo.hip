@@ -348,7 +348,7 @@ __global__ __launch_bounds__(kThreads) void logprob_backward_rows(
     if (VEC) {
       const int64_t nvec = vocab >> 3;
       for (int64_t i = tid; i < nvec; i += kThreads)
-        reinterpret_cast<uint4*>(gp)[i] = make_uint4(0, 0, 0, 0);
+        __builtin_nontemporal_store(u32x4_t{0u, 0u, 0u, 0u}, reinterpret_cast<u32x4_t*>(gp) + i);
       for (int64_t j = (nvec << 3) + tid; j < vocab; j += kThreads) gp[j] = 0;
     } else {
       for (int64_t j = tid; j < vocab; j += kThreads) gp[j] = 0;
@@ -358,10 +358,11 @@ __global__ __launch_bounds__(kThreads) void logprob_backward_rows(
   const float l2 = lse[row] * kLog2e;
   if (VEC) {
     const int64_t nvec = vocab >> 3;
-    for (int64_t i = tid; i < nvec; i += kThreads) {
-      const uint4 x = load_u4_stream(rp + (i << 3));
+    // kUnroll 16-byte loads in flight per lane; the gradient is streamed out
+    // with non-temporal stores.
+    auto grad8 = [&](const uint4 x, int64_t i) {
       const uint32_t w[4] = {x.x, x.y, x.z, x.w};
-      uint32_t o[4];
+      u32x4_t o;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const int64_t v0 = (i << 3) + 2 * k;
@@ -371,8 +372,17 @@ __global__ __launch_bounds__(kThreads) void logprob_backward_rows(
         if (v0 + 1 == id) g1 += c;
         o[k] = pack_bf16x2(g0, g1);
       }
-      reinterpret_cast<uint4*>(gp)[i] = make_uint4(o[0], o[1], o[2], o[3]);
+      __builtin_nontemporal_store(o, reinterpret_cast<u32x4_t*>(gp) + i);
+    };
+    int64_t i = tid;
+    for (; i + (kUnroll - 1) * kThreads < nvec; i += kUnroll * kThreads) {
+      uint4 x[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) x[u] = load_u4_stream(rp + ((i + u * kThreads) << 3));
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) grad8(x[u], i + u * kThreads);
     }
+    for (; i < nvec; i += kThreads) grad8(load_u4_stream(rp + (i << 3)), i);
     for (int64_t j = (nvec << 3) + tid; j < vocab; j += kThreads) {
       float g = -c * fast_exp2(fmaf(bf16_to_f32(rp[j]), kLog2e, -l2));
       if (j == id) g += c;
