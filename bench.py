@@ -359,7 +359,7 @@ def leg_rollout(torch, pkg, dev, new_tokens=1024, compare_tokens=64):
                                             top_k=None)
     out = {}
     # Short comparison against the reference path (same scheduler, torch attention).
-    for name in ("ours_short", "reference_path_short"):
+    for name in (("ours_short", "reference_path_short") if compare_tokens > 0 else ()):
         torch.manual_seed(1)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
@@ -473,6 +473,8 @@ def main() -> int:
     ap.add_argument("--legs", default="decode,grpo,store,prefill,rollout")
     ap.add_argument("--rollout-tokens", type=int, default=1024,
                     help="new tokens per sequence in the end-to-end rollout leg")
+    ap.add_argument("--rollout-compare-tokens", type=int, default=64,
+                    help="new tokens of the short ours-vs-reference-path comparison (0 skips it)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 1 GiB device copy (counter calibration)")
@@ -515,7 +517,8 @@ def main() -> int:
     if "prefill" in legs:
         results["prefill"] = leg_prefill(torch, pkg, W, dev, max(3, args.steps // 2), args.warmup)
     if "rollout" in legs:
-        results["rollout"] = leg_rollout(torch, pkg, dev, new_tokens=args.rollout_tokens)
+        results["rollout"] = leg_rollout(torch, pkg, dev, new_tokens=args.rollout_tokens,
+                                         compare_tokens=args.rollout_compare_tokens)
 
     cpu_grpo = None
     if not args.no_cpu and "grpo" in results:
@@ -569,13 +572,15 @@ def main() -> int:
             "loss_s": round(r["loss_s"], 3), "loss": r["loss"], "kv_blocks": r["num_blocks"],
             "preemptions": r.get("preemptions"), "engine_steps": r.get("steps"),
             "graph_decode_steps": r.get("graph_steps"),
-            "short_compare_64_tokens": {
+            "lookahead_decode_steps": r.get("lookahead_steps")}
+        if "ours_short" in r:
+            secondary["grpo_rollout"][f"short_compare_{args.rollout_compare_tokens}_tokens"] = {
                 "ours_tokens_per_s": round(r["ours_short"], 1),
                 "reference_path_tokens_per_s": round(r["reference_path_short"], 1),
                 "reference_path": "same scheduler; torch RMSNorm/RoPE/SwiGLU/store; attention = "
                                   f"{ReferencePath.attention_kind} over block-table-gathered K/V "
                                   "(flash-attn unavailable); eager decode",
-                "speedup": round(r["ours_short"] / r["reference_path_short"], 2)}}
+                "speedup": round(r["ours_short"] / r["reference_path_short"], 2)}
 
     if "decode" in results:
         d = results["decode"]
