@@ -20,16 +20,18 @@
 //     query l%16) is exactly the B-operand layout of the second product
 //     O^T = V^T P^T once two 16-key blocks are packed to bf16, so P never
 //     leaves registers.
-//   * V^T lives in LDS with the keys of each 32-key chunk permuted so that
-//     the 8 keys one lane needs for a V^T operand (keys 32c+4g..+3 and
-//     32c+16+4g..+3) are contiguous: one 16-byte LDS read per operand.
-//     Staging: a lane loads 4 consecutive keys x 8 dims, transposes them in
-//     registers and writes 8 x 8 bytes (one per dim); the 16 lanes of a
-//     write phase cover one dim row, so the writes do not conflict.
+//   * V is staged like K (row-major, 16-byte chunks, 256 contiguous bytes per
+//     16 lanes; rows padded to 288 bytes) and the V^T operand is read with
+//     gfx950's LDS transpose read (ds_read_b64_tr_b16): in a 16-lane group,
+//     lane r receives 16-bit element r % 4 of lane 4e + r / 4's 8 bytes as
+//     element e, so pointing lane i at V[kbase + i / 4][16 db + 4 (i % 4)]
+//     hands lane r the 4 keys kbase .. kbase+3 of dim 16 db + r.  Two such
+//     reads (keys 32c + 4g and 32c + 16 + 4g) form the 8 keys the B operand
+//     P^T packs for the lane, so no register transpose is needed.
 //   * Online softmax in fp32 (log2 domain); per query the 4 lanes holding
 //     its keys agree on the running max through two shuffles, while the
 //     running sum stays lane-partial until the end.
-//   * K / V^T tiles of 64 keys (one quarter page) are double-buffered in LDS:
+//   * K / V tiles of 64 keys (one quarter page) are double-buffered in LDS:
 //     the global loads for tile t+1 are in flight while tile t is computed.
 //   * Grid = (Hkv, query blocks, B): with 8 KV heads the KV head maps to the
 //     XCD, so all query blocks of one (sequence, KV head) share an L2.
@@ -47,17 +49,11 @@ constexpr int kThreads = 256;
 constexpr int kKeyTile = 64;
 constexpr int kWaveQ = 32;              // queries per wave (two MFMA column blocks)
 constexpr int kKPitch = kHeadDim + 8;   // bf16 per K row in LDS (272 B: 16 rows hit 16 distinct 4-bank groups)
-constexpr int kVtPitch = kKeyTile + 8;  // bf16 per V^T row in LDS (144 B, 16-B aligned rows)
+constexpr int kVPitch = kHeadDim + 16;  // bf16 per V row in LDS (288 B: 4 rows hit distinct 8-word spans)
+typedef __attribute__((ext_vector_type(4))) short v4s_t;
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
   return __builtin_bit_cast(bf16x8_t, u32x4_t{v.x, v.y, v.z, v.w});
-}
-
-// LDS position of key kk (0..63) inside a V^T row: within each 32-key chunk,
-// key 16h + 4g + r goes to 8g + 4h + r.
-__device__ __forceinline__ int vt_pos(int kk) {
-  const int c = kk >> 5, h = (kk >> 4) & 1, g = (kk >> 2) & 3, r = kk & 3;
-  return 32 * c + 8 * g + 4 * h + r;
 }
 
 template <int G>
@@ -73,7 +69,7 @@ void varlen_prefill_kernel(
   constexpr int kWavesPerHead = 4 / G;
   constexpr int kQB = kWaveQ * kWavesPerHead;  // queries per workgroup
   __shared__ __attribute__((aligned(16))) uint16_t sK[2][kKeyTile * kKPitch];
-  __shared__ __attribute__((aligned(16))) uint16_t sVt[2][kHeadDim * kVtPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t sV[2][kKeyTile * kVPitch];
 
   const int kvh = blockIdx.x;
   const int qblk = n_qblocks - 1 - (int)blockIdx.y;  // late (long) blocks first
@@ -119,24 +115,20 @@ void varlen_prefill_kernel(
   const int kend = max(0, min(Lk, diag + min(q0 + kQB, Lq)));
   const int n_tiles = (kend + kKeyTile - 1) / kKeyTile;
 
-  // Staging.  K: lane moves chunks c = tid + 256 i (key c / 16, dims
-  // 8 * (c % 16)), 256 contiguous bytes per 16 lanes.  V: lane (dc = tid / 16,
-  // kq = tid % 16) moves keys 4 kq .. 4 kq + 3 of dims 8 dc .. 8 dc + 7.
+  // Staging (K and V alike): lane moves chunks c = tid + 256 i (key c / 16,
+  // dims 8 * (c % 16)), 256 contiguous bytes per 16 lanes.
   // Addresses are a per-tile scalar base (the tile's first key row of this KV
   // head) plus a fixed 32-bit lane offset.  A tile never leaves its page, so
   // the loads are issued unconditionally; keys at or past kend are stale page
   // rows, masked in the scores, and their V rows are zeroed.  A tile whose
   // page-table entry is outside [0, num_blocks) is skipped in the compute.
   const int64_t row_elems = (int64_t)num_kv_heads * kHeadDim;
-  uint32_t k_off[4], v_off[4];
+  uint32_t st_off[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int c = tid + kThreads * i;
-    k_off[i] = (uint32_t)(((c >> 4) * row_elems + 8 * (c & 15)) * 2);
+    st_off[i] = (uint32_t)(((c >> 4) * row_elems + 8 * (c & 15)) * 2);
   }
-  const int v_dc = tid >> 4, v_kq = tid & 15;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) v_off[i] = (uint32_t)(((4 * v_kq + i) * row_elems + 8 * v_dc) * 2);
   uint4 kst[4], vst[4];
   bool tile_ok[2] = {false, false};
   int st_valid = 0;  // valid keys in the staged tile
@@ -148,9 +140,9 @@ void varlen_prefill_kernel(
     const char* kb = reinterpret_cast<const char*>(k_cache + row0 * row_elems + kvh * kHeadDim);
     const char* vb = reinterpret_cast<const char*>(v_cache + row0 * row_elems + kvh * kHeadDim);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) kst[i] = load_u4(kb + k_off[i]);
+    for (int i = 0; i < 4; ++i) kst[i] = load_u4(kb + st_off[i]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) vst[i] = load_u4(vb + v_off[i]);
+    for (int i = 0; i < 4; ++i) vst[i] = load_u4(vb + st_off[i]);
     st_valid = page_ok ? min(kKeyTile, kend - key0) : 0;
   };
   auto store_tile = [&](int buf) {
@@ -163,24 +155,13 @@ void varlen_prefill_kernel(
     if (st_valid < kKeyTile) {  // wave-uniform: zero V rows past the valid keys
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        if (4 * v_kq + i >= st_valid) vst[i] = make_uint4(0, 0, 0, 0);
+        if (((tid + kThreads * i) >> 4) >= st_valid) vst[i] = make_uint4(0, 0, 0, 0);
     }
     tile_ok[buf] = st_valid > 0;
-    const int pos = vt_pos(4 * v_kq);
-    const uint32_t w0[4] = {vst[0].x, vst[0].y, vst[0].z, vst[0].w};
-    const uint32_t w1[4] = {vst[1].x, vst[1].y, vst[1].z, vst[1].w};
-    const uint32_t w2[4] = {vst[2].x, vst[2].y, vst[2].z, vst[2].w};
-    const uint32_t w3[4] = {vst[3].x, vst[3].y, vst[3].z, vst[3].w};
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      // dims 8dc+2d (low halves) and 8dc+2d+1 (high halves) of keys 4kq..4kq+3
-      const uint32_t lo_e = __builtin_amdgcn_perm(w1[d], w0[d], 0x05040100u);
-      const uint32_t hi_e = __builtin_amdgcn_perm(w3[d], w2[d], 0x05040100u);
-      const uint32_t lo_o = __builtin_amdgcn_perm(w1[d], w0[d], 0x07060302u);
-      const uint32_t hi_o = __builtin_amdgcn_perm(w3[d], w2[d], 0x07060302u);
-      *reinterpret_cast<uint2*>(&sVt[buf][(8 * v_dc + 2 * d) * kVtPitch + pos]) = make_uint2(lo_e, hi_e);
-      *reinterpret_cast<uint2*>(&sVt[buf][(8 * v_dc + 2 * d + 1) * kVtPitch + pos]) =
-          make_uint2(lo_o, hi_o);
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid + kThreads * i;
+      *reinterpret_cast<uint4*>(&sV[buf][(c >> 4) * kVPitch + 8 * (c & 15)]) = vst[i];
     }
   };
 
@@ -290,28 +271,29 @@ void varlen_prefill_kernel(
       }
     }
 
-    // ---- O^T += V^T P^T over 8 blocks of 16 dims (operands read one block ahead) ----
-    const uint16_t* vbase = &sVt[buf][l16 * kVtPitch + 8 * g4];
-    bf16x8_t vop[2][2];
+    // ---- O^T += V^T P^T: V^T operands by LDS transpose reads ----
+    // Lane (r, g4) needs V[key][16 db + r] for keys 32c + 4g4 + 0..3 and
+    // 32c + 16 + 4g4 + 0..3; in each 16-lane group lane i points at
+    // V[kbase + i / 4][16 db + 4 (i % 4)].
+    {
+      const int vrow = 4 * g4 + (l16 >> 2);
+      const int vcol = 4 * (l16 & 3);
 #pragma unroll
-    for (int c = 0; c < 2; ++c)
-      vop[0][c] = as_bf16x8(*reinterpret_cast<const uint4*>(vbase + 32 * c));
+      for (int db = 0; db < 8; ++db) {
 #pragma unroll
-    for (int db = 0; db < 8; ++db) {
-      if (db + 1 < 8) {
+        for (int c = 0; c < 2; ++c) {
+          const uint16_t* p0 = &sV[buf][(32 * c + vrow) * kVPitch + 16 * db + vcol];
+          const v4s_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) v4s_t*)p0);
+          const v4s_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) v4s_t*)(p0 + 16 * kVPitch));
+          const bf16x8_t vop = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
-        for (int c = 0; c < 2; ++c)
-          vop[(db + 1) & 1][c] = as_bf16x8(*reinterpret_cast<const uint4*>(
-              vbase + (db + 1) * 16 * kVtPitch + 32 * c));
+          for (int j = 0; j < 2; ++j)
+            acc_o[j][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[j][c], acc_o[j][db], 0, 0, 0);
+        }
       }
-#pragma unroll
-      for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc_o[j][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop[db & 1][c], pop[j][c],
-                                                                 acc_o[j][db], 0, 0, 0);
     }
-
     }  // compute
     if (t + 1 < n_tiles) store_tile(buf ^ 1);
     __syncthreads();
