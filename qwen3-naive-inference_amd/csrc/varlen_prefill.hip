@@ -20,19 +20,30 @@
 //     query l%16) is exactly the B-operand layout of the second product
 //     O^T = V^T P^T once two 16-key blocks are packed to bf16, so P never
 //     leaves registers.
-//   * V is staged like K (row-major, 16-byte chunks, 256 contiguous bytes per
-//     16 lanes; rows padded to 288 bytes) and the V^T operand is read with
-//     gfx950's LDS transpose read (ds_read_b64_tr_b16): in a 16-lane group,
-//     lane r receives 16-bit element r % 4 of lane 4e + r / 4's 8 bytes as
-//     element e, so pointing lane i at V[kbase + i / 4][16 db + 4 (i % 4)]
-//     hands lane r the 4 keys kbase .. kbase+3 of dim 16 db + r.  Two such
-//     reads (keys 32c + 4g and 32c + 16 + 4g) form the 8 keys the B operand
-//     P^T packs for the lane, so no register transpose is needed.
+//   * K and V tiles are copied global -> LDS by the gfx950 direct loads
+//     (global_load_lds_dwordx4: a wave-wide instruction fills 1 KB of LDS,
+//     lane l at base + 16 l), so no registers or LDS stores stage them.
+//     Rows are 256 bytes (one KV head of a token) with the 16-byte chunks
+//     XOR-swizzled instead of padded: chunk c of K row r sits at c ^ (r % 16)
+//     (16 consecutive rows then hit 16 distinct 4-bank groups for the A
+//     operand reads), chunk c of V row r at c ^ 2 (r % 4); each lane fetches
+//     the logical chunk that its physical slot holds.
+//   * The V^T operand is read with gfx950's LDS transpose read
+//     (ds_read_b64_tr_b16): in a 16-lane group, lane r receives 16-bit
+//     element r % 4 of lane 4e + r / 4's 8 bytes as element e, so pointing
+//     lane i at V[kbase + i / 4][16 db + 4 (i % 4)] hands lane r the 4 keys
+//     kbase .. kbase+3 of dim 16 db + r.  Two such reads (keys 32c + 4g and
+//     32c + 16 + 4g) form the 8 keys the B operand P^T packs for the lane.
+//     These reads are issued as inline asm with explicit LDS-counter waits,
+//     one 16-dim block ahead: the compiler would otherwise wait for every
+//     outstanding direct load (the next tile's) before the first of them.
 //   * Online softmax in fp32 (log2 domain); per query the 4 lanes holding
 //     its keys agree on the running max through two shuffles, while the
 //     running sum stays lane-partial until the end.
 //   * K / V tiles of 64 keys (one quarter page) are double-buffered in LDS:
-//     the global loads for tile t+1 are in flight while tile t is computed.
+//     the direct loads of tile t+1 are in flight while tile t is computed.
+//     Keys past the workgroup's last visible key are stale page rows: their
+//     scores are masked and their V rows zeroed once the tile has landed.
 //   * Grid = (Hkv, query blocks, B): with 8 KV heads the KV head maps to the
 //     XCD, so all query blocks of one (sequence, KV head) share an L2.
 //     Query blocks are issued last-first, so the longest (causal) blocks
@@ -48,9 +59,8 @@ constexpr int kPage = 256;
 constexpr int kThreads = 256;
 constexpr int kKeyTile = 64;
 constexpr int kWaveQ = 32;              // queries per wave (two MFMA column blocks)
-constexpr int kKPitch = kHeadDim + 8;   // bf16 per K row in LDS (272 B: 16 rows hit 16 distinct 4-bank groups)
-constexpr int kVPitch = kHeadDim + 16;  // bf16 per V row in LDS (288 B: 4 rows hit distinct 8-word spans)
 typedef __attribute__((ext_vector_type(4))) short v4s_t;
+typedef __attribute__((ext_vector_type(2))) unsigned int v2u_t;
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
   return __builtin_bit_cast(bf16x8_t, u32x4_t{v.x, v.y, v.z, v.w});
@@ -68,8 +78,10 @@ void varlen_prefill_kernel(
     uint16_t* __restrict__ out, int64_t out_tok_stride, int64_t out_head_stride) {
   constexpr int kWavesPerHead = 4 / G;
   constexpr int kQB = kWaveQ * kWavesPerHead;  // queries per workgroup
-  __shared__ __attribute__((aligned(16))) uint16_t sK[2][kKeyTile * kKPitch];
-  __shared__ __attribute__((aligned(16))) uint16_t sV[2][kKeyTile * kVPitch];
+  // Unpadded 256-byte rows, 16-byte chunks XOR-swizzled: K chunk c of row r
+  // sits at c ^ (r % 16), V chunk c at c ^ 2 (r % 4).
+  __shared__ __attribute__((aligned(16))) uint16_t sK[2][kKeyTile * kHeadDim];
+  __shared__ __attribute__((aligned(16))) uint16_t sV[2][kKeyTile * kHeadDim];
 
   const int kvh = blockIdx.x;
   const int qblk = n_qblocks - 1 - (int)blockIdx.y;  // late (long) blocks first
@@ -115,24 +127,26 @@ void varlen_prefill_kernel(
   const int kend = max(0, min(Lk, diag + min(q0 + kQB, Lq)));
   const int n_tiles = (kend + kKeyTile - 1) / kKeyTile;
 
-  // Staging (K and V alike): lane moves chunks c = tid + 256 i (key c / 16,
-  // dims 8 * (c % 16)), 256 contiguous bytes per 16 lanes.
-  // Addresses are a per-tile scalar base (the tile's first key row of this KV
-  // head) plus a fixed 32-bit lane offset.  A tile never leaves its page, so
-  // the loads are issued unconditionally; keys at or past kend are stale page
-  // rows, masked in the scores, and their V rows are zeroed.  A tile whose
-  // page-table entry is outside [0, num_blocks) is skipped in the compute.
+  // Tile loads: addresses are a per-tile scalar base (the tile's first key
+  // row of this KV head) plus a fixed 32-bit lane offset.  A tile never
+  // leaves its page, so the loads are issued unconditionally; keys at or past
+  // kend are stale page rows, masked in the scores, and their V rows are
+  // zeroed.  A tile whose page-table entry is outside [0, num_blocks) is
+  // skipped in the compute.
   const int64_t row_elems = (int64_t)num_kv_heads * kHeadDim;
-  uint32_t st_off[4];
+  // Direct global -> LDS loads: wave w's instruction i fills rows 4q .. 4q+3
+  // (q = 4w + i) of a tile, lane l writing 16 bytes at row 4q + l / 16,
+  // physical chunk l % 16, fetched from the logical chunk the swizzle maps there.
+  uint32_t k_src[4], v_src[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int c = tid + kThreads * i;
-    st_off[i] = (uint32_t)(((c >> 4) * row_elems + 8 * (c & 15)) * 2);
+    const int row = 4 * (4 * wave + i) + (lane >> 4), pc = lane & 15;
+    k_src[i] = (uint32_t)((row * row_elems + 8 * (pc ^ (row & 15))) * 2);
+    v_src[i] = (uint32_t)((row * row_elems + 8 * (pc ^ ((row & 3) << 1))) * 2);
   }
-  uint4 kst[4], vst[4];
   bool tile_ok[2] = {false, false};
-  int st_valid = 0;  // valid keys in the staged tile
-  auto load_tile = [&](int t) {
+  int st_valid[2] = {0, 0};
+  auto load_tile = [&](int t, int buf) {
     const int key0 = t * kKeyTile;
     const int32_t blk = block_table[(int64_t)b * bt_stride + key0 / kPage];
     const bool page_ok = blk >= 0 && blk < num_blocks;
@@ -140,28 +154,24 @@ void varlen_prefill_kernel(
     const char* kb = reinterpret_cast<const char*>(k_cache + row0 * row_elems + kvh * kHeadDim);
     const char* vb = reinterpret_cast<const char*>(v_cache + row0 * row_elems + kvh * kHeadDim);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) kst[i] = load_u4(kb + st_off[i]);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) vst[i] = load_u4(vb + st_off[i]);
-    st_valid = page_ok ? min(kKeyTile, kend - key0) : 0;
+    for (int i = 0; i < 4; ++i) {
+      const int q4 = 4 * wave + i;
+      __builtin_amdgcn_global_load_lds(kb + k_src[i],
+          (__attribute__((address_space(3))) void*)&sK[buf][q4 * 4 * kHeadDim], 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vb + v_src[i],
+          (__attribute__((address_space(3))) void*)&sV[buf][q4 * 4 * kHeadDim], 16, 0, 0);
+    }
+    st_valid[buf] = page_ok ? min(kKeyTile, kend - key0) : 0;
+    tile_ok[buf] = st_valid[buf] > 0;
   };
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = tid + kThreads * i;
-      const int key = c >> 4, dchunk = c & 15;
-      *reinterpret_cast<uint4*>(&sK[buf][key * kKPitch + 8 * dchunk]) = kst[i];
-    }
-    if (st_valid < kKeyTile) {  // wave-uniform: zero V rows past the valid keys
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (((tid + kThreads * i) >> 4) >= st_valid) vst[i] = make_uint4(0, 0, 0, 0);
-    }
-    tile_ok[buf] = st_valid > 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = tid + kThreads * i;
-      *reinterpret_cast<uint4*>(&sV[buf][(c >> 4) * kVPitch + 8 * (c & 15)]) = vst[i];
+  // After the tile's loads have landed (every lane waited, then a barrier):
+  // zero V rows past the valid keys (0 * stale NaN would poison O).
+  auto fix_tile = [&](int buf) {
+    if (st_valid[buf] < kKeyTile) {
+      for (int c = tid; c < kKeyTile * 16; c += kThreads)
+        if ((c >> 4) >= st_valid[buf])
+          *reinterpret_cast<uint4*>(&sV[buf][(c >> 4) * kHeadDim + 8 * (c & 15)]) = make_uint4(0, 0, 0, 0);
+      __syncthreads();
     }
   };
 
@@ -173,16 +183,15 @@ void varlen_prefill_kernel(
 #pragma unroll
     for (int db = 0; db < 8; ++db) acc_o[j][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  if (n_tiles > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
+  if (n_tiles > 0) load_tile(0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  if (n_tiles > 0) fix_tile(0);
 
   for (int t = 0; t < n_tiles; ++t) {
     const int buf = t & 1;
     const bool compute = tile_ok[buf];  // wave-uniform
-    if (t + 1 < n_tiles) load_tile(t + 1);
+    if (t + 1 < n_tiles) load_tile(t + 1, buf ^ 1);
     if (compute) {
 
     // ---- S^T = K Q^T for 4 blocks of 16 keys x 2 blocks of 16 queries ----
@@ -193,18 +202,20 @@ void varlen_prefill_kernel(
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) s[j][kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    const uint16_t* kbase = &sK[buf][l16 * kKPitch + 8 * g4];
+    // row 16 kb + l16, logical chunk 4c + g4 -> physical (4c + g4) ^ l16
+    const uint16_t* kbase = &sK[buf][l16 * kHeadDim];
+    auto kchunk = [&](int kb, int c) {
+      return as_bf16x8(*reinterpret_cast<const uint4*>(kbase + kb * 16 * kHeadDim + 8 * ((4 * c + g4) ^ l16)));
+    };
     bf16x8_t kop[2][4];
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
-      kop[0][kb] = as_bf16x8(*reinterpret_cast<const uint4*>(kbase + kb * 16 * kKPitch));
+    for (int kb = 0; kb < 4; ++kb) kop[0][kb] = kchunk(kb, 0);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       if (c + 1 < 4) {
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb)
-          kop[(c + 1) & 1][kb] = as_bf16x8(
-              *reinterpret_cast<const uint4*>(kbase + kb * 16 * kKPitch + 32 * (c + 1)));
+          kop[(c + 1) & 1][kb] = kchunk(kb, c + 1);
       }
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
@@ -272,22 +283,39 @@ void varlen_prefill_kernel(
     }
 
     // ---- O^T += V^T P^T: V^T operands by LDS transpose reads ----
-    // Lane (r, g4) needs V[key][16 db + r] for keys 32c + 4g4 + 0..3 and
-    // 32c + 16 + 4g4 + 0..3; in each 16-lane group lane i points at
-    // V[kbase + i / 4][16 db + 4 (i % 4)].
+    // Issued as inline asm with explicit LDS-counter waits, so the reads of
+    // tile t do not wait for the direct loads of tile t+1 (still in flight).
     {
       const int vrow = 4 * g4 + (l16 >> 2);
-      const int vcol = 4 * (l16 & 3);
-#pragma unroll
-      for (int db = 0; db < 8; ++db) {
+      const int vsw = ((l16 >> 2) & 3) << 1;
+      const uint32_t vb0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)&sV[buf][vrow * kHeadDim] + 8 * (l16 & 1);
+      auto vaddr = [&](int db, int c) -> uint32_t {
+        const int lc = 2 * db + ((l16 & 3) >> 1);
+        return vb0 + (uint32_t)(c * 32 * kHeadDim * 2 + 16 * (lc ^ vsw));
+      };
+      v2u_t r[2][2][2];  // [stage][c][lo/hi]
+      auto issue = [&](int db, int st) {
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-          const uint16_t* p0 = &sV[buf][(32 * c + vrow) * kVPitch + 16 * db + vcol];
-          const v4s_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (__attribute__((address_space(3))) v4s_t*)p0);
-          const v4s_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (__attribute__((address_space(3))) v4s_t*)(p0 + 16 * kVPitch));
-          const bf16x8_t vop = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+          const uint32_t ad = vaddr(db, c);
+          asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r[st][c][0]) : "v"(ad) : "memory");
+          asm volatile("ds_read_b64_tr_b16 %0, %1 offset:4096" : "=v"(r[st][c][1]) : "v"(ad) : "memory");
+        }
+      };
+      issue(0, 0);
+#pragma unroll
+      for (int db = 0; db < 8; ++db) {
+        const int st = db & 1;
+        if (db + 1 < 8) {
+          issue(db + 1, st ^ 1);
+          asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(r[st][0][0]), "+v"(r[st][0][1]), "+v"(r[st][1][0]), "+v"(r[st][1][1]) :: "memory");
+        } else {
+          asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[st][0][0]), "+v"(r[st][0][1]), "+v"(r[st][1][0]), "+v"(r[st][1][1]) :: "memory");
+        }
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const u32x4_t w4 = {r[st][c][0].x, r[st][c][0].y, r[st][c][1].x, r[st][c][1].y};
+          const bf16x8_t vop = __builtin_bit_cast(bf16x8_t, w4);
 #pragma unroll
           for (int j = 0; j < 2; ++j)
             acc_o[j][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[j][c], acc_o[j][db], 0, 0, 0);
@@ -295,8 +323,9 @@ void varlen_prefill_kernel(
       }
     }
     }  // compute
-    if (t + 1 < n_tiles) store_tile(buf ^ 1);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    if (t + 1 < n_tiles) fix_tile(buf ^ 1);
   }
 
   // ---- normalise and write O[query][dims] ----
