@@ -38,8 +38,10 @@
 //     one 16-dim block ahead: the compiler would otherwise wait for every
 //     outstanding direct load (the next tile's) before the first of them.
 //   * Online softmax in fp32 (log2 domain); per query the 4 lanes holding
-//     its keys agree on the running max through two shuffles, while the
-//     running sum stays lane-partial until the end.
+//     its keys agree on the running max through two shuffles.  The running
+//     sum of P is one more MFMA per 32 keys (A = a 16 x 32 block whose row 0
+//     is all ones), so it sums exactly the bf16 P the O^T product uses and
+//     costs no VALU adds.
 //   * K / V tiles of 64 keys (one quarter page) are double-buffered in LDS:
 //     the direct loads of tile t+1 are in flight while tile t is computed.
 //     Keys past the workgroup's last visible key are stale page rows: their
@@ -176,7 +178,8 @@ void varlen_prefill_kernel(
   };
 
   float m_run[2] = {kNegBig, kNegBig};  // running max (log2 domain) per query
-  float l_run[2] = {0.f, 0.f};          // lane-partial running sums
+  f32x4_t acc_l[2];                     // row 0 (lanes 0-15): running sum of P (bf16) per query
+  acc_l[0] = acc_l[1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   f32x4_t acc_o[2][8];                  // O^T[dim 16*db + 4*g4 + r][query]
 #pragma unroll
   for (int j = 0; j < 2; ++j)
@@ -260,7 +263,7 @@ void varlen_prefill_kernel(
         const float m_new = need ? m_cand : m_run[j];
         const float alpha = fast_exp2(m_run[j] - m_new);
         m_run[j] = m_new;
-        l_run[j] *= alpha;
+        acc_l[j] *= alpha;
 #pragma unroll
         for (int db = 0; db < 8; ++db) acc_o[j][db] *= alpha;
       }
@@ -275,10 +278,7 @@ void varlen_prefill_kernel(
           p[4 + r] = fast_exp2(fmaf(s[j][2 * c + 1][r], scale_log2, neg_m));
         }
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          l_run[j] += p[e];
-          pop[j][c][e] = (__bf16)p[e];
-        }
+        for (int e = 0; e < 8; ++e) pop[j][c][e] = (__bf16)p[e];
       }
     }
 
@@ -322,6 +322,16 @@ void varlen_prefill_kernel(
         }
       }
     }
+      // Row sums of P by MFMA: A = 16 x 32 with row 0 all ones.
+      {
+        const __bf16 one = (l16 == 0) ? (__bf16)1.0f : (__bf16)0.0f;
+        const bf16x8_t ones = {one, one, one, one, one, one, one, one};
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc_l[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pop[j][c], acc_l[j], 0, 0, 0);
+      }
     }  // compute
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -331,8 +341,7 @@ void varlen_prefill_kernel(
   // ---- normalise and write O[query][dims] ----
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    float l_tot = l_run[j] + shfl_xor_f32(l_run[j], 16);
-    l_tot += shfl_xor_f32(l_tot, 32);
+    const float l_tot = __shfl(acc_l[j][0], l16, 64);  // row 0 lives in lanes 0-15
     const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
     const int my_q = wq0 + 16 * j + l16;
     if (my_q < Lq) {
