@@ -185,3 +185,15 @@ def test_decode_balanced_schedule_head_layouts(pkg, gpu, hq, hkv):
     out = _decode(pkg, gpu, w)
     torch.cuda.synchronize()
     _check(out, w)
+
+
+def test_decode_more_than_1024_sequences_uses_split_schedule(pkg, gpu):
+    """Beyond 1024 sequences the balanced schedule's in-LDS prefix scan does
+    not apply and the per-(sequence, KV head) split takes over."""
+    g = torch.Generator().manual_seed(63)
+    lens = torch.randint(0, 300, (1100,), generator=g).tolist()
+    w = _ragged(64, lens)
+    print("[decode] 1100 seqs", flush=True)
+    out = _decode(pkg, gpu, w)
+    torch.cuda.synchronize()
+    _check(out, w)
