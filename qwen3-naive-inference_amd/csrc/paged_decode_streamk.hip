@@ -374,6 +374,77 @@ __global__ __launch_bounds__(kThreads) void decode_streamk_merge(
   }
 }
 
+// The same combination for large batches (each sequence shared by a few
+// workgroups): one workgroup per sequence, a 16-lane group per query head
+// (a lane owns 8 output dims) walking the sharing workgroups, four slots in
+// flight; no LDS.
+template <int HKV, int G>
+__global__ __launch_bounds__(kThreads) void decode_streamk_merge_seq(
+    int batch, int n_wg, const float* __restrict__ ws, uint16_t* __restrict__ out,
+    int64_t out_seq_stride, int64_t out_head_stride) {
+  constexpr int HQ = HKV * G;
+  constexpr int kGroups = kThreads / 16;
+  const int32_t* ws_off = reinterpret_cast<const int32_t*>(ws + (int64_t)n_wg * 2 * HQ * kSlotStride);
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x, lane16 = tid & 15, grp = tid >> 4;
+  const int64_t total = ws_off[batch];
+  const int64_t sb = ws_off[b], se = ws_off[b + 1];
+  uint16_t* o_seq = out + (int64_t)b * out_seq_stride;
+  const int d0 = lane16 * 8;
+  if (se == sb) {  // empty sequence attends to nothing: zeros, as flash-attn
+    for (int qh = grp; qh < HQ; qh += kGroups)
+      *reinterpret_cast<uint4*>(o_seq + (int64_t)qh * out_head_stride + d0) = make_uint4(0, 0, 0, 0);
+    return;
+  }
+  const int64_t w0 = owner_of(sb, total, n_wg);
+  const int64_t w1 = owner_of(se - 1, total, n_wg);
+  if (w0 == w1) return;  // written directly by its only workgroup
+  for (int qh = grp; qh < HQ; qh += kGroups) {
+    float M = kNegBig, Ls = 0.f, A[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) A[e] = 0.f;
+    for (int64_t wb = w0; wb <= w1; wb += 4) {
+      float mw[4], lw[4];
+      f32x4_t a0[4], a1[4];
+      bool ok[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        // A workgroup with an empty step range owns no slot; w0 owns step sb,
+        // so its slot 0 is always written and stands in for such entries.
+        const int64_t ww = wb + j;
+        const int64_t r0 = range_start(ww, total, n_wg);
+        ok[j] = ww <= w1 && r0 != range_start(ww + 1, total, n_wg);
+        const int64_t slot = ok[j] ? ww * 2 + ((r0 >= sb) ? 0 : 1) : w0 * 2;
+        const float* p = ws + (slot * HQ + qh) * kSlotStride;
+        mw[j] = p[kHeadDim];
+        lw[j] = p[kHeadDim + 1];
+        a0[j] = *reinterpret_cast<const f32x4_t*>(p + d0);
+        a1[j] = *reinterpret_cast<const f32x4_t*>(p + d0 + 4);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (!ok[j]) continue;
+        const float mn = fmaxf(M, mw[j]);
+        const float s1 = fast_exp2(M - mn), s2 = fast_exp2(mw[j] - mn);
+        Ls = Ls * s1 + lw[j] * s2;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          A[e] = A[e] * s1 + a0[j][e] * s2;
+          A[4 + e] = A[4 + e] * s1 + a1[j][e] * s2;
+        }
+        M = mn;
+      }
+    }
+    const float inv = Ls > 0.f ? 1.f / Ls : 0.f;
+    uint4 pk;
+    pk.x = pack_bf16x2(A[0] * inv, A[1] * inv);
+    pk.y = pack_bf16x2(A[2] * inv, A[3] * inv);
+    pk.z = pack_bf16x2(A[4] * inv, A[5] * inv);
+    pk.w = pack_bf16x2(A[6] * inv, A[7] * inv);
+    *reinterpret_cast<uint4*>(o_seq + (int64_t)qh * out_head_stride + d0) = pk;
+  }
+}
+
 }  // namespace
 
 namespace qmi {
@@ -429,8 +500,15 @@ static int launch(const uint16_t* q, int64_t qs, int64_t qh, const uint16_t* kc,
                      scale_log2, out, os, oh, ws);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
-  hipLaunchKernelGGL((decode_streamk_merge<HKV, G>), dim3((unsigned)batch, (unsigned)(HKV * G)),
-                     dim3(kThreads), 0, s, (int)batch, (int)n_wg, ws, out, os, oh);
+  // Small batches: sequences are shared by many workgroups, so one merge
+  // workgroup per (sequence, head) reads 16 slots at once; large batches:
+  // a few slots per sequence, one workgroup per sequence.
+  if (batch >= 128)
+    hipLaunchKernelGGL((decode_streamk_merge_seq<HKV, G>), dim3((unsigned)batch), dim3(kThreads), 0, s,
+                       (int)batch, (int)n_wg, ws, out, os, oh);
+  else
+    hipLaunchKernelGGL((decode_streamk_merge<HKV, G>), dim3((unsigned)batch, (unsigned)(HKV * G)),
+                       dim3(kThreads), 0, s, (int)batch, (int)n_wg, ws, out, os, oh);
   QMI_RETURN_LAUNCH_STATUS();
 }
 

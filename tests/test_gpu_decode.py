@@ -163,13 +163,16 @@ def test_decode_balanced_schedule_ragged_with_empty(pkg, gpu):
 
 
 def test_decode_balanced_schedule_large_batch(pkg, gpu):
-    """More sequences than one workgroup per sequence: 300 short contexts."""
+    """More sequences than one workgroup per sequence: 300 short contexts
+    (the per-sequence merge), some of them empty."""
     g = torch.Generator().manual_seed(61)
     lens = torch.randint(1, 700, (300,), generator=g).tolist()
+    lens[5] = lens[77] = lens[299] = 0
     w = _ragged(62, lens)
     print("[decode] balanced 300 seqs", flush=True)
     out = _decode(pkg, gpu, w)
     torch.cuda.synchronize()
+    assert out[[5, 77, 299]].abs().max().item() == 0.0
     _check(out, w)
 
 
