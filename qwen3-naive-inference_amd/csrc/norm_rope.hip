@@ -41,11 +41,13 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_rows(
   const int tid = threadIdx.x;
   const int nvec = n >> 3;
   float v[kMaxVec][8];
+  uint4 wv[kMaxVec];  // weight chunks, loaded with the row so the tail has no dependent load
   float ss = 0.f;
 #pragma unroll
   for (int k = 0; k < kMaxVec; ++k) {
     const int c = tid + k * kNormThreads;
     if (c < nvec) {
+      wv[k] = load_u4(w + 8 * c);
       const uint4 a = load_u4(x + row * x_stride + 8 * c);
       const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
@@ -81,11 +83,12 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_rows(
   for (int k = 0; k < kMaxVec; ++k) {
     const int c = tid + k * kNormThreads;
     if (c < nvec) {
+      const uint32_t ww[4] = {wv[k].x, wv[k].y, wv[k].z, wv[k].w};
       uint32_t o[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        o[e] = pack_bf16x2(v[k][2 * e] * inv * bf16_to_f32(w[8 * c + 2 * e]),
-                           v[k][2 * e + 1] * inv * bf16_to_f32(w[8 * c + 2 * e + 1]));
+        o[e] = pack_bf16x2(v[k][2 * e] * inv * bf16_lo(ww[e]),
+                           v[k][2 * e + 1] * inv * bf16_hi(ww[e]));
       *reinterpret_cast<uint4*>(y + row * y_stride + 8 * c) = make_uint4(o[0], o[1], o[2], o[3]);
     }
   }
@@ -113,19 +116,23 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
   const int64_t tok = item / heads;
   const int h = (int)(item - tok * heads);
   const bool is_q = h < n_q_heads;
+  // Every load is issued before the reduction: position -> cos/sin is the
+  // only dependent pair.
+  int64_t pos = positions[tok];
   const uint16_t* src = qkv + tok * qkv_stride + (int64_t)h * D;
+  const uint16_t* w = is_q ? q_w : k_w;
   const float x1 = bf16_to_f32(src[lane]);
   const float x2 = bf16_to_f32(src[lane + HALF]);
-  const float ss = wave_sum(x1 * x1 + x2 * x2);
-  const float inv = rsqrtf(ss / (float)D + eps);
-  const uint16_t* w = is_q ? q_w : k_w;
-  // QK-norm output is bf16 in the reference before RoPE reads it.
-  const float n1 = bf16_to_f32(f32_to_bf16(x1 * inv * bf16_to_f32(w[lane])));
-  const float n2 = bf16_to_f32(f32_to_bf16(x2 * inv * bf16_to_f32(w[lane + HALF])));
-  int64_t pos = positions[tok];
+  const float w1 = bf16_to_f32(w[lane]);
+  const float w2 = bf16_to_f32(w[lane + HALF]);
   pos = pos < 0 ? 0 : (pos >= max_pos ? max_pos - 1 : pos);
   const float c = cos_sin[pos * D + lane];
   const float s = cos_sin[pos * D + HALF + lane];
+  const float ss = wave_sum(x1 * x1 + x2 * x2);
+  const float inv = rsqrtf(ss / (float)D + eps);
+  // QK-norm output is bf16 in the reference before RoPE reads it.
+  const float n1 = bf16_to_f32(f32_to_bf16(x1 * inv * w1));
+  const float n2 = bf16_to_f32(f32_to_bf16(x2 * inv * w2));
   const float o1 = n1 * c - n2 * s;
   const float o2 = n2 * c + n1 * s;
   const uint16_t b1 = f32_to_bf16(o1), b2 = f32_to_bf16(o2);
