@@ -46,10 +46,11 @@
 //     the direct loads of tile t+1 are in flight while tile t is computed.
 //     Keys past the workgroup's last visible key are stale page rows: their
 //     scores are masked and their V rows zeroed once the tile has landed.
-//   * Grid = (Hkv, query blocks, B): with 8 KV heads the KV head maps to the
+//   * Grid = (Hkv, B, query blocks): with 8 KV heads the KV head maps to the
 //     XCD, so all query blocks of one (sequence, KV head) share an L2.
-//     Query blocks are issued last-first, so the longest (causal) blocks
-//     start first.
+//     Query blocks are the slowest grid dimension and are issued last-first:
+//     the late (longest, causal) blocks of every sequence start before any
+//     early block, which shortens the tail of a launch.
 #include "qmi_common.h"
 
 namespace {
@@ -86,8 +87,8 @@ void varlen_prefill_kernel(
   __shared__ __attribute__((aligned(16))) uint16_t sV[2][kKeyTile * kHeadDim];
 
   const int kvh = blockIdx.x;
-  const int qblk = n_qblocks - 1 - (int)blockIdx.y;  // late (long) blocks first
-  const int b = blockIdx.z;
+  const int b = blockIdx.y;
+  const int qblk = n_qblocks - 1 - (int)blockIdx.z;  // late (long) blocks first
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
@@ -389,7 +390,7 @@ extern "C" int qmi_varlen_prefill_attention(
   if (n_qblocks > 65535 || batch > 65535 || num_kv_heads > 65535 || bt_width > (1 << 22))
     return QMI_E_UNSUPPORTED;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const dim3 grid((unsigned)num_kv_heads, (unsigned)n_qblocks, (unsigned)batch);
+  const dim3 grid((unsigned)num_kv_heads, (unsigned)batch, (unsigned)n_qblocks);
   const float scale_log2 = scale * kLog2e;
 #define QMI_PREFILL_CASE(GG)                                                                      \
   case GG:                                                                                        \
