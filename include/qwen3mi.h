@@ -119,15 +119,35 @@ int qmi_paged_decode_attention(const uint16_t* q, int64_t q_seq_stride, int64_t 
  * block_size 256, num_q_heads / num_kv_heads in {1, 2, 4}.  Keys on pages
  * whose table entry is outside [0, num_blocks) contribute nothing (as in
  * decode); num_blocks == 0 is rejected (QMI_E_BAD_SHAPE).
+ *
+ * Long key ranges: key ranges can be split into pieces run by separate
+ * workgroups, whose fp32 partial results go to `workspace` and are merged by
+ * a second kernel on the same stream.  split_keys == 0 (automatic) splits
+ * only launches with fewer than 256 (query block, sequence, KV head) work
+ * items, e.g. a short chunk after a long cached prefix, into enough pieces
+ * to give about 512 workgroups (at most 16 per item); split_keys > 0 (a
+ * multiple of 64) cuts key ranges into pieces of that many keys (at most 16
+ * per item) whatever the launch size.  max_seqlen_k (the longest Lk) only
+ * sizes the split; any value gives the same result.  Pass a workspace of at
+ * least qmi_varlen_prefill_workspace_bytes(...) bytes (16-byte aligned);
+ * with a smaller one (or NULL) nothing is split.  Calls that share one
+ * workspace must not overlap.
  */
+int64_t qmi_varlen_prefill_workspace_bytes(int64_t batch, int64_t max_seqlen_q,
+                                           int64_t max_seqlen_k, int64_t num_q_heads,
+                                           int64_t num_kv_heads, int64_t bt_width,
+                                           int64_t split_keys);
+
 int qmi_varlen_prefill_attention(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride,
                                  const uint16_t* k_cache, const uint16_t* v_cache,
                                  int64_t num_blocks, int64_t block_size,
                                  int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
                                  const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
                                  const int32_t* block_table, int64_t bt_stride, int64_t bt_width,
-                                 int64_t batch, int64_t max_seqlen_q, int64_t total_q, float scale,
-                                 uint16_t* out, int64_t out_tok_stride, int64_t out_head_stride,
+                                 int64_t batch, int64_t max_seqlen_q, int64_t max_seqlen_k,
+                                 int64_t total_q, float scale, uint16_t* out,
+                                 int64_t out_tok_stride, int64_t out_head_stride,
+                                 float* workspace, int64_t workspace_bytes, int64_t split_keys,
                                  void* stream);
 
 /*

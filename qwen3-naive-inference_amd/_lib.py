@@ -36,14 +36,17 @@ SIGNATURES: dict[str, tuple] = {
         _c_i64, _c_f32,                  # batch, scale
         _c_p, _c_i64, _c_i64,            # out, strides
         _c_p, _c_i64, _c_i64, _c_p]),    # workspace, bytes, pages_per_split, stream
+    "qmi_varlen_prefill_workspace_bytes": (_c_i64, [_c_i64] * 7),
     "qmi_varlen_prefill_attention": (ctypes.c_int, [
         _c_p, _c_i64, _c_i64,            # q, strides
         _c_p, _c_p, _c_i64, _c_i64,      # caches, num_blocks, block_size
         _c_i64, _c_i64, _c_i64,          # heads, kv heads, head_dim
         _c_p, _c_p,                      # cu_seqlens_q / k
         _c_p, _c_i64, _c_i64,            # block_table, stride, width
-        _c_i64, _c_i64, _c_i64, _c_f32,  # batch, max_seqlen_q, total_q, scale
-        _c_p, _c_i64, _c_i64, _c_p]),    # out, strides, stream
+        _c_i64, _c_i64, _c_i64,          # batch, max_seqlen_q, max_seqlen_k
+        _c_i64, _c_f32,                  # total_q, scale
+        _c_p, _c_i64, _c_i64,            # out, strides
+        _c_p, _c_i64, _c_i64, _c_p]),    # workspace, bytes, split_keys, stream
     "qmi_rms_norm": (ctypes.c_int, [_c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_f32,
                                     _c_p]),
     "qmi_add_rms_norm": (ctypes.c_int, [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p,

@@ -51,6 +51,16 @@
 //     Query blocks are the slowest grid dimension and are issued last-first:
 //     the late (longest, causal) blocks of every sequence start before any
 //     early block, which shortens the tail of a launch.
+//   * Long key ranges are split when a launch has too few work items to fill
+//     the GPU (e.g. one sequence with a long cached prefix): a (query block,
+//     sequence, KV head) item whose keys span more than split_tiles tiles is
+//     cut into at most n_split equal tile ranges (grid z = part x query
+//     blocks), each run by its own workgroup.
+//     Split pieces store the unnormalised O rows, the running max and the
+//     row sum (fp32) to a workspace, and varlen_prefill_merge combines them;
+//     items that are not split write their output directly.
+#include <algorithm>
+
 #include "qmi_common.h"
 
 namespace {
@@ -69,6 +79,34 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
   return __builtin_bit_cast(bf16x8_t, u32x4_t{v.x, v.y, v.z, v.w});
 }
 
+// Work item geometry shared by the attention and merge kernels.
+struct Item {
+  int q_start, Lq, Lk, diag, n_tiles, n_parts;
+};
+
+__device__ __forceinline__ Item item_geometry(const int32_t* __restrict__ cu_q,
+                                              const int32_t* __restrict__ cu_k, int b, int q0,
+                                              int qb, int64_t total_q, int bt_width, int n_split,
+                                              int split_tiles) {
+  Item it;
+  // Rows outside [0, total_q) of q / out are never touched, whatever cu_q holds.
+  it.q_start = max(0, cu_q[b]);
+  it.Lq = (int)max((int64_t)0, min((int64_t)cu_q[b + 1], total_q) - it.q_start);
+  it.Lk = max(0, min(cu_k[b + 1] - cu_k[b], bt_width * kPage));
+  it.diag = it.Lk - it.Lq;  // query i sees keys j <= i + diag
+  // Keys the block needs: up to its last query's diagonal.
+  const int kend = max(0, min(it.Lk, it.diag + min(q0 + qb, it.Lq)));
+  it.n_tiles = (kend + kKeyTile - 1) / kKeyTile;
+  it.n_parts = max(1, min(n_split, (it.n_tiles + split_tiles - 1) / split_tiles));
+  return it;
+}
+
+// Workspace of a split launch: per (item, part) slot, 128 rows of O (fp32,
+// 128 dims, unnormalised), then, after all slots, (max, sum) per row.
+__device__ __forceinline__ int64_t part_slot(int kvh, int b, int qblk, int part, int n_split) {
+  return (((int64_t)qblk * gridDim.y + b) * gridDim.x + kvh) * n_split + part;
+}
+
 template <int G>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void varlen_prefill_kernel(
@@ -78,7 +116,8 @@ void varlen_prefill_kernel(
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k,
     const int32_t* __restrict__ block_table, int64_t bt_stride, int bt_width,
     int n_qblocks, int64_t total_q, float scale_log2,
-    uint16_t* __restrict__ out, int64_t out_tok_stride, int64_t out_head_stride) {
+    uint16_t* __restrict__ out, int64_t out_tok_stride, int64_t out_head_stride,
+    int n_split, int split_tiles, float* __restrict__ ws) {
   constexpr int kWavesPerHead = 4 / G;
   constexpr int kQB = kWaveQ * kWavesPerHead;  // queries per workgroup
   // Unpadded 256-byte rows, 16-byte chunks XOR-swizzled: K chunk c of row r
@@ -88,21 +127,19 @@ void varlen_prefill_kernel(
 
   const int kvh = blockIdx.x;
   const int b = blockIdx.y;
-  const int qblk = n_qblocks - 1 - (int)blockIdx.z;  // late (long) blocks first
+  const int qblk = n_qblocks - 1 - (int)(blockIdx.z % n_qblocks);  // late (long) blocks first
+  const int part = (int)(blockIdx.z / n_qblocks);
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int l16 = lane & 15;
   const int g4 = lane >> 4;
 
-  // Rows outside [0, total_q) of q / out are never touched, whatever cu_q holds.
-  const int q_start = max(0, cu_q[b]);
-  const int Lq = (int)max((int64_t)0, min((int64_t)cu_q[b + 1], total_q) - q_start);
-  int Lk = cu_k[b + 1] - cu_k[b];
-  Lk = max(0, min(Lk, bt_width * kPage));
   const int q0 = qblk * kQB;
-  if (q0 >= Lq) return;  // uniform over the workgroup
-  const int diag = Lk - Lq;  // query i sees keys j <= i + diag
+  const Item item = item_geometry(cu_q, cu_k, b, q0, kQB, total_q, bt_width, n_split, split_tiles);
+  // Both exits are uniform over the workgroup.
+  if (q0 >= item.Lq || part >= item.n_parts) return;
+  const int q_start = item.q_start, Lq = item.Lq, Lk = item.Lk, diag = item.diag;
 
   const int qh = kvh * G + wave / kWavesPerHead;
   const int wq0 = q0 + (wave % kWavesPerHead) * kWaveQ;
@@ -126,9 +163,11 @@ void varlen_prefill_kernel(
     }
   }
 
-  // Keys this workgroup needs: up to the last query's diagonal.
+  // Keys this workgroup needs: up to the last query's diagonal; part `part`
+  // of n_parts takes tiles [t_begin, t_end).
   const int kend = max(0, min(Lk, diag + min(q0 + kQB, Lq)));
-  const int n_tiles = (kend + kKeyTile - 1) / kKeyTile;
+  const int t_begin = (int)((int64_t)part * item.n_tiles / item.n_parts);
+  const int t_end = (int)((int64_t)(part + 1) * item.n_tiles / item.n_parts);
 
   // Tile loads: addresses are a per-tile scalar base (the tile's first key
   // row of this KV head) plus a fixed 32-bit lane offset.  A tile never
@@ -187,15 +226,15 @@ void varlen_prefill_kernel(
 #pragma unroll
     for (int db = 0; db < 8; ++db) acc_o[j][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  if (n_tiles > 0) load_tile(0, 0);
+  if (t_begin < t_end) load_tile(t_begin, 0);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (n_tiles > 0) fix_tile(0);
+  if (t_begin < t_end) fix_tile(0);
 
-  for (int t = 0; t < n_tiles; ++t) {
-    const int buf = t & 1;
+  for (int t = t_begin; t < t_end; ++t) {
+    const int buf = (t - t_begin) & 1;
     const bool compute = tile_ok[buf];  // wave-uniform
-    if (t + 1 < n_tiles) load_tile(t + 1, buf ^ 1);
+    if (t + 1 < t_end) load_tile(t + 1, buf ^ 1);
     if (compute) {
 
     // ---- S^T = K Q^T for 4 blocks of 16 keys x 2 blocks of 16 queries ----
@@ -336,7 +375,28 @@ void varlen_prefill_kernel(
     }  // compute
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (t + 1 < n_tiles) fix_tile(buf ^ 1);
+    if (t + 1 < t_end) fix_tile(buf ^ 1);
+  }
+
+  if (item.n_parts > 1) {
+    // ---- split item: store the unnormalised rows, their max and sum ----
+    const int64_t slot = part_slot(kvh, b, qblk, part, n_split);
+    const int64_t n_slots = (int64_t)n_qblocks * gridDim.y * gridDim.x * n_split;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const float l_tot = __shfl(acc_l[j][0], l16, 64);
+      const int row = wave * kWaveQ + 16 * j + l16;  // row of the item: head-major, then query
+      if (wq0 + 16 * j + l16 < Lq) {
+        float* orow = ws + (slot * 128 + row) * kHeadDim;
+#pragma unroll
+        for (int db = 0; db < 8; ++db)
+          *reinterpret_cast<f32x4_t*>(orow + db * 16 + 4 * g4) = acc_o[j][db];
+        if (g4 == 0)
+          *reinterpret_cast<float2*>(ws + n_slots * 128 * kHeadDim + (slot * 128 + row) * 2) =
+              make_float2(m_run[j], l_tot);
+      }
+    }
+    return;
   }
 
   // ---- normalise and write O[query][dims] ----
@@ -358,19 +418,125 @@ void varlen_prefill_kernel(
   }
 }
 
+// Combines the parts of split items: O = sum_p 2^(m_p - M) O_p / sum_p 2^(m_p - M) l_p
+// with M = max_p m_p (m in the scaled log2 domain of the attention kernel).
+// Grid = (Hkv, B, 8 x query blocks): workgroup z covers rows 16 (z / n_qblocks)
+// .. +15 of its item; thread t merges dims 8 (t % 16) .. +7 of row t / 16.
+constexpr int kMergeRowGroups = 8;
+
+template <int G>
+__global__ __launch_bounds__(kThreads) void varlen_prefill_merge(
+    const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k, int bt_width,
+    int n_qblocks, int64_t total_q, uint16_t* __restrict__ out, int64_t out_tok_stride,
+    int64_t out_head_stride, int n_split, int split_tiles, const float* __restrict__ ws) {
+  constexpr int kQB = 128 / G;
+  const int kvh = blockIdx.x, b = blockIdx.y;
+  const int qblk = n_qblocks - 1 - (int)(blockIdx.z % n_qblocks);
+  const int rgrp = (int)(blockIdx.z / n_qblocks);
+  const int q0 = qblk * kQB;
+  const Item item = item_geometry(cu_q, cu_k, b, q0, kQB, total_q, bt_width, n_split, split_tiles);
+  if (q0 >= item.Lq || item.n_parts <= 1) return;
+  const int row = rgrp * 16 + (threadIdx.x >> 4);
+  const int d0 = 8 * (threadIdx.x & 15);
+  const int qry = q0 + row % kQB;
+  if (qry >= item.Lq) return;
+  // part_slot() indexes with the attention grid's x / y, which this grid shares.
+  const int64_t slot0 = part_slot(kvh, b, qblk, 0, n_split);
+  const int64_t n_slots = (int64_t)n_qblocks * gridDim.y * gridDim.x * n_split;
+  const float* ml = ws + n_slots * 128 * kHeadDim;
+  float m_max = kNegBig;
+  for (int p = 0; p < item.n_parts; ++p) m_max = fmaxf(m_max, ml[((slot0 + p) * 128 + row) * 2]);
+  float l_sum = 0.f, o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int p = 0; p < item.n_parts; ++p) {
+    const float2 mlp = *reinterpret_cast<const float2*>(ml + ((slot0 + p) * 128 + row) * 2);
+    const float* op = ws + ((slot0 + p) * 128 + row) * kHeadDim + d0;
+    const f32x4_t a = *reinterpret_cast<const f32x4_t*>(op);
+    const f32x4_t c = *reinterpret_cast<const f32x4_t*>(op + 4);
+    const float w = fast_exp2(mlp.x - m_max);
+    l_sum = fmaf(w, mlp.y, l_sum);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      o[e] = fmaf(w, a[e], o[e]);
+      o[4 + e] = fmaf(w, c[e], o[4 + e]);
+    }
+  }
+  const float inv = l_sum > 0.f ? 1.0f / l_sum : 0.f;
+  const int qh = kvh * G + row / kQB;
+  uint16_t* orow = out + (int64_t)(item.q_start + qry) * out_tok_stride + (int64_t)qh * out_head_stride + d0;
+  *reinterpret_cast<uint2*>(orow) = make_uint2(pack_bf16x2(o[0] * inv, o[1] * inv), pack_bf16x2(o[2] * inv, o[3] * inv));
+  *reinterpret_cast<uint2*>(orow + 4) = make_uint2(pack_bf16x2(o[4] * inv, o[5] * inv), pack_bf16x2(o[6] * inv, o[7] * inv));
+}
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Parts per item for a launch.  split_keys == 0 (automatic): a launch with
+// fewer items than kSplitMaxItems has its longest key range cut into enough
+// parts to give ~kSplitTargetItems workgroups (bounded by kMaxSplit and by the
+// tile count); larger launches are not split, since their workgroups already
+// fill every CU and a split only adds the partial traffic and the merge.
+// split_keys > 0: parts of split_keys keys whatever the launch size.
+// Returns the number of parts and the tiles per part.
+constexpr int64_t kSplitMaxItems = 256;
+constexpr int64_t kSplitTargetItems = 512;
+constexpr int64_t kMaxSplit = 16;
+
+void prefill_splits(int64_t batch, int64_t n_qblocks, int64_t num_kv_heads, int64_t max_seqlen_k,
+                    int64_t bt_width, int64_t split_keys, int64_t* n_split, int64_t* split_tiles) {
+  *n_split = 1;
+  *split_tiles = 1 << 30;
+  const int64_t items = batch * n_qblocks * num_kv_heads;
+  const int64_t max_keys = std::min(std::max<int64_t>(max_seqlen_k, 0), bt_width * kPage);
+  const int64_t max_tiles = (max_keys + kKeyTile - 1) / kKeyTile;
+  if (max_tiles <= 1) return;
+  if (split_keys > 0) {
+    *split_tiles = split_keys / kKeyTile;
+    *n_split = std::min(kMaxSplit, (max_tiles + *split_tiles - 1) / *split_tiles);
+  } else if (items < kSplitMaxItems) {
+    const int64_t want = (kSplitTargetItems + items - 1) / items;
+    *n_split = std::min({kMaxSplit, want, max_tiles});
+    *split_tiles = (max_tiles + *n_split - 1) / *n_split;
+  }
+  if (*n_split <= 1) {
+    *n_split = 1;
+    *split_tiles = 1 << 30;
+  }
+}
+
+int64_t split_workspace_bytes(int64_t batch, int64_t n_qblocks, int64_t num_kv_heads, int64_t n_split) {
+  if (n_split <= 1) return 0;
+  return batch * n_qblocks * num_kv_heads * n_split * 128 * (kHeadDim + 2) * (int64_t)sizeof(float);
+}
+
 }  // namespace
+
+extern "C" int64_t qmi_varlen_prefill_workspace_bytes(int64_t batch, int64_t max_seqlen_q,
+                                                      int64_t max_seqlen_k, int64_t num_q_heads,
+                                                      int64_t num_kv_heads, int64_t bt_width,
+                                                      int64_t split_keys) {
+  if (batch <= 0 || max_seqlen_q <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 ||
+      num_q_heads % num_kv_heads != 0 || bt_width <= 0)
+    return 0;
+  if (split_keys < 0 || split_keys % kKeyTile) return 0;
+  const int64_t G = num_q_heads / num_kv_heads;
+  if (G != 1 && G != 2 && G != 4) return 0;
+  const int64_t n_qblocks = (max_seqlen_q + 128 / G - 1) / (128 / G);
+  int64_t n_split, split_tiles;
+  prefill_splits(batch, n_qblocks, num_kv_heads, max_seqlen_k, bt_width, split_keys, &n_split,
+                 &split_tiles);
+  return split_workspace_bytes(batch, n_qblocks, num_kv_heads, n_split);
+}
 
 extern "C" int qmi_varlen_prefill_attention(
     const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride, const uint16_t* k_cache,
     const uint16_t* v_cache, int64_t num_blocks, int64_t block_size, int64_t num_q_heads,
     int64_t num_kv_heads, int64_t head_dim, const int32_t* cu_seqlens_q,
     const int32_t* cu_seqlens_k, const int32_t* block_table, int64_t bt_stride, int64_t bt_width,
-    int64_t batch, int64_t max_seqlen_q, int64_t total_q, float scale, uint16_t* out,
-    int64_t out_tok_stride, int64_t out_head_stride, void* stream) {
+    int64_t batch, int64_t max_seqlen_q, int64_t max_seqlen_k, int64_t total_q, float scale,
+    uint16_t* out, int64_t out_tok_stride, int64_t out_head_stride, float* workspace,
+    int64_t workspace_bytes, int64_t split_keys, void* stream) {
   if (batch < 0 || max_seqlen_q < 0 || num_blocks < 0 || bt_width < 0) return QMI_E_BAD_SHAPE;
-  if (total_q < 0) return QMI_E_BAD_SHAPE;
+  if (total_q < 0 || workspace_bytes < 0) return QMI_E_BAD_SHAPE;
+  if (split_keys < 0 || split_keys % kKeyTile) return QMI_E_BAD_SHAPE;
   if (batch == 0 || max_seqlen_q == 0 || total_q == 0) return QMI_OK;
   if (num_blocks == 0) return QMI_E_BAD_SHAPE;  // a pool without pages
   if (!q || !k_cache || !v_cache || !cu_seqlens_q || !cu_seqlens_k || !block_table || !out)
@@ -389,16 +555,31 @@ extern "C" int qmi_varlen_prefill_attention(
   const int64_t n_qblocks = (max_seqlen_q + qb - 1) / qb;
   if (n_qblocks > 65535 || batch > 65535 || num_kv_heads > 65535 || bt_width > (1 << 22))
     return QMI_E_UNSUPPORTED;
+  int64_t n_split, split_tiles;
+  prefill_splits(batch, n_qblocks, num_kv_heads, max_seqlen_k, bt_width, split_keys, &n_split,
+                 &split_tiles);
+  // Without room for the parts the launch runs unsplit (same result).
+  if (n_split > 1 && (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 15u) ||
+                      workspace_bytes < split_workspace_bytes(batch, n_qblocks, num_kv_heads, n_split)))
+    n_split = 1;
+  if (n_qblocks * n_split > 65535 || n_qblocks * kMergeRowGroups > 65535) n_split = 1;
+  if (n_split == 1) split_tiles = 1 << 30;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const dim3 grid((unsigned)num_kv_heads, (unsigned)batch, (unsigned)n_qblocks);
+  const dim3 grid((unsigned)num_kv_heads, (unsigned)batch, (unsigned)(n_qblocks * n_split));
+  const dim3 merge_grid((unsigned)num_kv_heads, (unsigned)batch, (unsigned)(n_qblocks * kMergeRowGroups));
   const float scale_log2 = scale * kLog2e;
+  float* ws = n_split > 1 ? workspace : nullptr;
 #define QMI_PREFILL_CASE(GG)                                                                      \
   case GG:                                                                                        \
     hipLaunchKernelGGL(varlen_prefill_kernel<GG>, grid, dim3(kThreads), 0, s, q, q_tok_stride,   \
                        q_head_stride, k_cache, v_cache, num_blocks, (int)num_kv_heads,            \
                        cu_seqlens_q, cu_seqlens_k, block_table, bt_stride, (int)bt_width,         \
                        (int)n_qblocks, total_q, scale_log2, out, out_tok_stride,                  \
-                       out_head_stride);                                                          \
+                       out_head_stride, (int)n_split, (int)split_tiles, ws);                      \
+    if (n_split > 1)                                                                              \
+      hipLaunchKernelGGL(varlen_prefill_merge<GG>, merge_grid, dim3(kThreads), 0, s,              \
+                         cu_seqlens_q, cu_seqlens_k, (int)bt_width, (int)n_qblocks, total_q, out,  \
+                         out_tok_stride, out_head_stride, (int)n_split, (int)split_tiles, ws);    \
     break;
   switch (G) {
     QMI_PREFILL_CASE(1)

@@ -155,7 +155,8 @@ def varlen_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: to
                              cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor,
                              max_seqlen_q: int, max_seqlen_k: int, softmax_scale: float,
                              causal: bool = True, block_table: torch.Tensor | None = None,
-                             out: torch.Tensor | None = None) -> torch.Tensor:
+                             out: torch.Tensor | None = None, *,
+                             split_keys: int = 0) -> torch.Tensor:
     """Varlen causal attention of the new tokens over their paged K/V.
 
     Argument order and meaning follow the reference call
@@ -164,8 +165,13 @@ def varlen_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: to
     block_table=...)``.  ``q``: ``[Tq, Hq, 128]`` bf16; caches
     ``[num_blocks, 256, Hkv, 128]``; ``cu_seqlens_*``: int32 ``[B+1]``;
     ``block_table``: int32 ``[B, W]``.  Returns ``[Tq, Hq, 128]`` bf16.
-    ``max_seqlen_k`` is accepted for signature parity (the kernel reads the
-    per-sequence key counts from ``cu_seqlens_k``).
+    The kernel reads the per-sequence key counts from ``cu_seqlens_k``;
+    ``max_seqlen_k`` only sizes the split of long key ranges across
+    workgroups: with ``split_keys=0`` launches with fewer than 256 (query
+    block, sequence, KV head) items are split automatically (e.g. a short
+    chunk after a long cached prefix); ``split_keys > 0`` forces pieces of
+    that many keys.  The fp32 partials go to a workspace from the torch
+    allocator and are merged by a second kernel.
     """
     if not causal:
         raise ValueError("only causal=True is supported (the reference always passes it)")
@@ -207,11 +213,18 @@ def varlen_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: to
             raise ValueError("out must be [Tq, Hq, D] with unit stride along D")
     if bsz == 0 or tq == 0 or int(max_seqlen_q) == 0:
         return out
+    split_keys = int(split_keys)
+    if split_keys < 0 or split_keys % 64:
+        raise ValueError(f"split_keys must be 0 or a positive multiple of 64, got {split_keys}")
+    ws_bytes = lib().qmi_varlen_prefill_workspace_bytes(
+        bsz, int(max_seqlen_q), int(max_seqlen_k), hq, hkv, bt.shape[1], split_keys)
+    ws = (torch.empty(ws_bytes // 4, dtype=torch.float32, device=q.device) if ws_bytes > 0
+          else None)
     st = lib().qmi_varlen_prefill_attention(
         q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(), nb, bs,
         hq, hkv, d, cq.data_ptr(), ck.data_ptr(), bt.data_ptr(), bt.stride(0), bt.shape[1], bsz,
-        int(max_seqlen_q), tq, float(softmax_scale), out.data_ptr(), out.stride(0), out.stride(1),
-        stream_handle(q.device))
+        int(max_seqlen_q), int(max_seqlen_k), tq, float(softmax_scale), out.data_ptr(),
+        out.stride(0), out.stride(1), _ptr(ws), ws_bytes, split_keys, stream_handle(q.device))
     check(st, "varlen_prefill_attention")
     return out
 

@@ -209,3 +209,132 @@ def test_prefill_rejects_empty_pool(pkg, gpu):
     bt = torch.zeros(1, 1, dtype=torch.int32, device=gpu)
     with pytest.raises((ValueError, RuntimeError)):
         pkg.kernels.varlen_prefill_attention(q, kc, kc, cu, cu, 4, 4, SCALE, True, bt)
+
+
+def _run_split(pkg, gpu, q, kc, vc, cu_q, cu_k, bt, split_keys, max_k=None):
+    cq = torch.tensor(cu_q, dtype=torch.int32)
+    ck = torch.tensor(cu_k, dtype=torch.int32)
+    max_q = max(cu_q[i + 1] - cu_q[i] for i in range(len(cu_q) - 1))
+    if max_k is None:
+        max_k = max(cu_k[i + 1] - cu_k[i] for i in range(len(cu_k) - 1))
+    out = pkg.kernels.varlen_prefill_attention(q.to(gpu), kc.to(gpu), vc.to(gpu), cq.to(gpu),
+                                               ck.to(gpu), max_q, max_k, SCALE, True, bt.to(gpu),
+                                               split_keys=split_keys)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("split_keys", [64, 128, 320, 1024])
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (8, 8), (16, 4)])
+def test_prefill_split_key_ranges(pkg, gpu, split_keys, hq, hkv):
+    """Key ranges split across workgroups and merged give the oracle's result:
+    decode-like rows, a prefix-cached chunk, a full causal prompt, an empty
+    sequence and a short one, with pieces from one tile up."""
+    lens_q = [1, 200, 1300, 0, 37]
+    lens_k = [1500, 900, 1300, 3, 37]
+    cu_q, cu_k = [0], [0]
+    for a, c in zip(lens_q, lens_k):
+        cu_q.append(cu_q[-1] + a)
+        cu_k.append(cu_k[-1] + c)
+    kc, vc, bt = _pool(40 + split_keys + hq, lens_k, hkv=hkv)
+    g = torch.Generator().manual_seed(41 + split_keys)
+    q = torch.randn(cu_q[-1], hq, 128, generator=g).to(torch.bfloat16)
+    print(f"[prefill] split_keys={split_keys} gqa {hq}/{hkv}", flush=True)
+    n_ws = pkg._lib.lib().qmi_varlen_prefill_workspace_bytes(5, 1300, 1500, hq, hkv, bt.shape[1],
+                                                             split_keys)
+    assert n_ws > 0  # the launch is split
+    out = _run_split(pkg, gpu, q, kc, vc, cu_q, cu_k, bt, split_keys)
+    _check(out, q, kc, vc, cu_q, cu_k, bt)
+    whole = _run_split(pkg, gpu, q, kc, vc, cu_q, cu_k, bt, 1 << 20)
+    assert (out.float() - whole.float()).abs().max().item() <= 1e-2
+
+
+def test_prefill_split_any_max_seqlen_k(pkg, gpu):
+    """max_seqlen_k only sizes the split: too small (no split) and far too
+    large (more pieces than tiles for short rows) both give the oracle's result."""
+    lens_k = [1100, 700]
+    cu_q, cu_k = [0, 300, 400], [0, 1100, 1800]
+    kc, vc, bt = _pool(50, lens_k)
+    g = torch.Generator().manual_seed(51)
+    q = torch.randn(400, 16, 128, generator=g).to(torch.bfloat16)
+    print("[prefill] split with any max_seqlen_k", flush=True)
+    ref = OA.varlen_prefill(q, kc, vc, cu_q, cu_k, bt, SCALE)
+    for max_k in (1, 1100, 50_000):
+        out = _run_split(pkg, gpu, q, kc, vc, cu_q, cu_k, bt, 128, max_k=max_k)
+        assert (out.float().cpu() - ref).abs().max().item() <= TOL, max_k
+
+
+def test_prefill_split_unmapped_page(pkg, gpu):
+    """Keys on an unmapped page (table entry -1) inside a split key range
+    contribute nothing: 300 queries at the end of a 1100-key sequence whose
+    third page (keys 512..767) is unmapped match fp32 attention over the other
+    keys under the same causal mask."""
+    L, Lq = 1100, 300
+    kc, vc, bt = _pool(52, [L])
+    bt[0, 2] = -1
+    g = torch.Generator().manual_seed(53)
+    q = torch.randn(Lq, 16, 128, generator=g).to(torch.bfloat16)
+    print("[prefill] split over an unmapped page", flush=True)
+    out = _run_split(pkg, gpu, q, kc, vc, [0, Lq], [0, L], bt, 128)
+    keys = torch.arange(L)
+    pages = bt[0, keys // 256].long()
+    mapped = pages >= 0
+    rows = pages.clamp(min=0) * 256 + keys % 256
+    k = kc.reshape(-1, 8, 128)[rows].float()  # [L, 8, 128]
+    v = vc.reshape(-1, 8, 128)[rows].float()
+    qi = torch.arange(Lq)[:, None] + (L - Lq)
+    visible = (keys[None, :] <= qi) & mapped[None, :]
+    ref = torch.empty(Lq, 16, 128)
+    for h in range(16):
+        sc = (q[:, h].float() @ k[:, h // 2].T) * SCALE
+        sc = sc.masked_fill(~visible, float("-inf"))
+        ref[:, h] = torch.softmax(sc, dim=-1) @ v[:, h // 2]
+    assert (out.float().cpu() - ref).abs().max().item() <= TOL
+    whole = _run_split(pkg, gpu, q, kc, vc, [0, Lq], [0, L], bt, 1 << 20)
+    assert (out.float() - whole.float()).abs().max().item() <= 1e-2
+
+
+def test_prefill_split_needs_workspace(pkg, gpu):
+    """Through the C ABI: without a workspace the launch runs unsplit and
+    gives exactly the unsplit result."""
+    import ctypes
+    L = 900
+    kc, vc, bt = _pool(60, [L])
+    g = torch.Generator().manual_seed(61)
+    q = torch.randn(L, 16, 128, generator=g).to(torch.bfloat16).to(gpu)
+    kcg, vcg, btg = kc.to(gpu), vc.to(gpu), bt.to(gpu)
+    cu = torch.tensor([0, L], dtype=torch.int32, device=gpu)
+    print("[prefill] split without workspace", flush=True)
+    whole = pkg.kernels.varlen_prefill_attention(q, kcg, vcg, cu, cu, L, L, SCALE, True, btg,
+                                                 split_keys=1 << 20)
+    out = torch.empty_like(whole)
+    lib = pkg._lib.lib()
+    st = lib.qmi_varlen_prefill_attention(
+        q.data_ptr(), q.stride(0), q.stride(1), kcg.data_ptr(), vcg.data_ptr(), kcg.shape[0], 256,
+        16, 8, 128, cu.data_ptr(), cu.data_ptr(), btg.data_ptr(), btg.stride(0), btg.shape[1], 1,
+        L, L, L, SCALE, out.data_ptr(), out.stride(0), out.stride(1), None, 0, 64,
+        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    assert st == 0
+    assert torch.equal(out, whole)
+    with pytest.raises(ValueError):
+        pkg.kernels.varlen_prefill_attention(q, kcg, vcg, cu, cu, L, L, SCALE, True, btg,
+                                             split_keys=100)
+
+
+@pytest.mark.parametrize("lq,prefix,hq,hkv", [(1, 4095, 16, 8), (64, 4000, 16, 8), (200, 3000, 16, 4),
+                                               (300, 2000, 8, 8)])
+def test_prefill_auto_split_long_prefix(pkg, gpu, lq, prefix, hq, hkv):
+    """A lone short chunk after a long cached prefix has a handful of work
+    items, so the automatic mode splits its key range; the result matches the
+    oracle and the unsplit launch."""
+    L = prefix + lq
+    kc, vc, bt = _pool(70 + lq, [L], hkv=hkv)
+    g = torch.Generator().manual_seed(71 + lq)
+    q = torch.randn(lq, hq, 128, generator=g).to(torch.bfloat16)
+    print(f"[prefill] auto split lq={lq} prefix={prefix} gqa {hq}/{hkv}", flush=True)
+    assert pkg._lib.lib().qmi_varlen_prefill_workspace_bytes(1, lq, L, hq, hkv, bt.shape[1], 0) > 0
+    out = _run_split(pkg, gpu, q, kc, vc, [0, lq], [0, L], bt, 0)
+    _check(out, q, kc, vc, [0, lq], [0, L], bt)
+    whole = _run_split(pkg, gpu, q, kc, vc, [0, lq], [0, L], bt, 1 << 20)
+    assert (out.float() - whole.float()).abs().max().item() <= 1e-2
