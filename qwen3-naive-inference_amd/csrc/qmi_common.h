@@ -78,19 +78,42 @@ __device__ __forceinline__ float shfl_xor_f32(float x, int mask) {
   return __shfl_xor(x, mask, 64);
 }
 
-__device__ __forceinline__ float wave_sum(float x) {
-  x = row16_sum(x);
-  x += shfl_xor_f32(x, 16);
-  x += shfl_xor_f32(x, 32);
-  return x;
+// Lane pairs {l, l ^ 16} and {l, l ^ 32} through the gfx950 VALU lane swaps
+// (v_permlane16_swap / v_permlane32_swap, no LDS round trip): every lane gets
+// the pair's two values as (lower lane's, upper lane's), so a commutative
+// combine of the two gives bit-identical results on both lanes.
+struct LanePair {
+  float lo, hi;
+};
+
+__device__ __forceinline__ LanePair lane_pair16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return {__uint_as_float(r[0]), __uint_as_float(r[1])};
 }
 
-__device__ __forceinline__ float wave_max(float x) {
-  x = row16_max(x);
-  x = fmaxf(x, shfl_xor_f32(x, 16));
-  x = fmaxf(x, shfl_xor_f32(x, 32));
-  return x;
+__device__ __forceinline__ LanePair lane_pair32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return {__uint_as_float(r[0]), __uint_as_float(r[1])};
 }
+
+// Max / sum over the four lanes l, l ^ 16, l ^ 32, l ^ 48 (one per DPP row).
+__device__ __forceinline__ float rows4_max(float x) {
+  LanePair p = lane_pair16(x);
+  x = fmaxf(p.lo, p.hi);
+  p = lane_pair32(x);
+  return fmaxf(p.lo, p.hi);
+}
+
+__device__ __forceinline__ float rows4_sum(float x) {
+  LanePair p = lane_pair16(x);
+  x = p.lo + p.hi;
+  p = lane_pair32(x);
+  return p.lo + p.hi;
+}
+
+__device__ __forceinline__ float wave_sum(float x) { return rows4_sum(row16_sum(x)); }
+
+__device__ __forceinline__ float wave_max(float x) { return rows4_max(row16_max(x)); }
 
 // Merge two (max, sum-of-exp2) pairs kept in the log2 domain.
 __device__ __forceinline__ void lse2_merge(float& m, float& s, float m2, float s2) {

@@ -38,7 +38,7 @@
 //     one 16-dim block ahead: the compiler would otherwise wait for every
 //     outstanding direct load (the next tile's) before the first of them.
 //   * Online softmax in fp32 (log2 domain); per query the 4 lanes holding
-//     its keys agree on the running max through two shuffles.  The running
+//     its keys agree on the running max through two VALU lane swaps.  The running
 //     sum of P is one more MFMA per 32 keys (A = a 16 x 32 block whose row 0
 //     is all ones), so it sums exactly the bf16 P the O^T product uses and
 //     costs no VALU adds.
@@ -295,8 +295,7 @@ void varlen_prefill_kernel(
 #pragma unroll
       for (int kb = 1; kb < 4; ++kb)
         tmax = fmaxf(tmax, fmaxf(fmaxf(s[j][kb][0], s[j][kb][1]), fmaxf(s[j][kb][2], s[j][kb][3])));
-      tmax = fmaxf(tmax, shfl_xor_f32(tmax, 16));
-      tmax = fmaxf(tmax, shfl_xor_f32(tmax, 32));
+      tmax = rows4_max(tmax);
       const float m_cand = tmax * scale_log2;
       const bool need = m_cand > m_run[j] + 8.f;
       if (__ballot(need) != 0ull) {  // wave-uniform
