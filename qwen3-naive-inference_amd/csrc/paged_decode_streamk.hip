@@ -43,6 +43,18 @@ template <int HKV> constexpr int kStepTokens = kTokGroups<HKV> * kTok;   // divi
 constexpr int kSlotStride = kHeadDim + 4;      // acc[128], m, l, pad (per q head)
 constexpr int kMaxSeqScan = 1024;              // batch limit of the in-LDS prefix scan
 
+// Workgroups that take part: the launch is sized from the block-table width,
+// before the context lengths are known, so a short total would leave most
+// workgroups with an empty range, which the merge would still have to walk
+// past.  At most one workgroup per step takes part (the rest exit at once);
+// longer pieces for small totals measured slower (the split loses more than
+// the merge gains).
+constexpr int64_t kMinWgSteps = 1;
+__device__ __forceinline__ int64_t active_wgs(int64_t total, int64_t n_wg) {
+  const int64_t want = (total + kMinWgSteps - 1) / kMinWgSteps;
+  return want < 1 ? 1 : (want < n_wg ? want : n_wg);
+}
+
 __device__ __forceinline__ int64_t range_start(int64_t w, int64_t total, int64_t n_wg) {
   return w * total / n_wg;
 }
@@ -130,8 +142,10 @@ void decode_streamk_split(
   }
   const int64_t total = off[batch];
   if (total == 0) return;
-  const int64_t s_begin = range_start(w, total, n_wg);
-  const int64_t s_end = range_start(w + 1, total, n_wg);
+  const int64_t n_act = active_wgs(total, n_wg);
+  if (w >= n_act) return;
+  const int64_t s_begin = range_start(w, total, n_act);
+  const int64_t s_end = range_start(w + 1, total, n_act);
   if (s_begin >= s_end) return;
 
   // First sequence of the range (binary search over the exclusive offsets).
@@ -327,16 +341,17 @@ __global__ __launch_bounds__(kThreads) void decode_streamk_merge(
     if (tid < kHeadDim) o_row[tid] = 0;
     return;
   }
-  const int64_t w0 = owner_of(sb, total, n_wg);
-  const int64_t w1 = owner_of(se - 1, total, n_wg);
+  const int64_t n_act = active_wgs(total, n_wg);
+  const int64_t w0 = owner_of(sb, total, n_act);
+  const int64_t w1 = owner_of(se - 1, total, n_act);
   if (w0 == w1) return;  // written directly by its only workgroup
   const int d0 = lane16 * 8;
   float M = kNegBig, Ls = 0.f, A[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) A[e] = 0.f;
   for (int64_t ww = w0 + grp; ww <= w1; ww += kGroups) {
-    const int64_t r0 = range_start(ww, total, n_wg);
-    if (r0 == range_start(ww + 1, total, n_wg)) continue;  // empty range: owns no slot
+    const int64_t r0 = range_start(ww, total, n_act);
+    if (r0 == range_start(ww + 1, total, n_act)) continue;  // empty range: owns no slot
     const int slot = (r0 >= sb) ? 0 : 1;
     const float* p = ws + ((ww * 2 + slot) * HQ + qh) * kSlotStride;
     const float mw = p[kHeadDim], lw = p[kHeadDim + 1];
@@ -396,8 +411,9 @@ __global__ __launch_bounds__(kThreads) void decode_streamk_merge_seq(
       *reinterpret_cast<uint4*>(o_seq + (int64_t)qh * out_head_stride + d0) = make_uint4(0, 0, 0, 0);
     return;
   }
-  const int64_t w0 = owner_of(sb, total, n_wg);
-  const int64_t w1 = owner_of(se - 1, total, n_wg);
+  const int64_t n_act = active_wgs(total, n_wg);
+  const int64_t w0 = owner_of(sb, total, n_act);
+  const int64_t w1 = owner_of(se - 1, total, n_act);
   if (w0 == w1) return;  // written directly by its only workgroup
   for (int qh = grp; qh < HQ; qh += kGroups) {
     float M = kNegBig, Ls = 0.f, A[8];
@@ -412,8 +428,8 @@ __global__ __launch_bounds__(kThreads) void decode_streamk_merge_seq(
         // A workgroup with an empty step range owns no slot; w0 owns step sb,
         // so its slot 0 is always written and stands in for such entries.
         const int64_t ww = wb + j;
-        const int64_t r0 = range_start(ww, total, n_wg);
-        ok[j] = ww <= w1 && r0 != range_start(ww + 1, total, n_wg);
+        const int64_t r0 = range_start(ww, total, n_act);
+        ok[j] = ww <= w1 && r0 != range_start(ww + 1, total, n_act);
         const int64_t slot = ok[j] ? ww * 2 + ((r0 >= sb) ? 0 : 1) : w0 * 2;
         const float* p = ws + (slot * HQ + qh) * kSlotStride;
         mw[j] = p[kHeadDim];
