@@ -13,7 +13,8 @@ on the 32x512x151936 loss step, the KV store at 65,536 tokens, the varlen
 paged prefill on the prefix-cache chunk workload (MFMA TFLOP/s), and the CPU
 oracle (the CPU restatement of the reference semantics) timed on this host.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--legs decode1,decode,grpo,store,prefill,rollout]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+                       [--legs decode1,decode,grpo,store,prefill,norm_rope,host,rollout]
        [--no-cpu] [--calibrate-copy]
 """
 from __future__ import annotations
@@ -84,6 +85,23 @@ def timed_launches(torch, fn_list, steps, warmup):
     return total, per
 
 
+def graph_us_per_call(torch, fn, steps, warmup, per_graph=20):
+    """GPU µs per call of ``fn``: ``per_graph`` calls captured in one HIP graph,
+    replayed; for launches shorter than the host-side cost of a call."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(per_graph):
+            fn()
+    reps = max(2, steps // 2)
+    total_ms, _ = timed_launches(torch, [graph.replay], reps, max(1, warmup))
+    return total_ms * 1e3 / (reps * per_graph)
+
+
 # ---------------------------------------------------------------------------
 def leg_decode(torch, pkg, W, dev, steps, warmup, layers=28):
     log(f"decode: generating {layers}-layer pools (B=64, ctx U[1024,4096])")
@@ -144,7 +162,7 @@ def leg_grpo(torch, pkg, W, dev, steps, warmup):
     return out
 
 
-def leg_store(torch, pkg, dev, steps, warmup, n_tok=65536):
+def leg_store(torch, pkg, dev, steps, warmup, n_tok=65536, cpu=True):
     log(f"store: {n_tok} tokens")
     g = torch.Generator(device=dev)
     g.manual_seed(0)
@@ -159,11 +177,142 @@ def leg_store(torch, pkg, dev, steps, warmup, n_tok=65536):
     total_ms, per = timed_launches(torch, [fn], steps, warmup)
     nbytes = 2 * 2 * key.numel() * 2 + slots.numel() * 4
     ms = statistics.mean(per)
-    return dict(avg_launch_us=ms * 1e3, gbs=nbytes / (ms * 1e-3) / 1e9, bytes_per_launch=nbytes,
-                tokens=n_tok)
+    res = dict(avg_launch_us=ms * 1e3, gbs=nbytes / (ms * 1e-3) / 1e9, bytes_per_launch=nbytes,
+               tokens=n_tok)
+    if cpu:
+        # The oracle's per-token store (one row copy per token, as the reference
+        # launches one program per token) on the host, over an 8,192-token sample.
+        from oracle import paged as OP
+        torch.set_num_threads(os.cpu_count() or 1)
+        n_s = 8192
+        k_c, v_c = key[:n_s].cpu(), val[:n_s].cpu()
+        kc_c = torch.zeros((nb, 256, 8, 128), dtype=torch.bfloat16)
+        vc_c = torch.zeros_like(kc_c)
+        sl = slots[:n_s].cpu()
+        times = []
+        for _ in range(3):
+            t = time.perf_counter()
+            OP.store_kvcache(k_c, v_c, kc_c, vc_c, sl)
+            times.append(time.perf_counter() - t)
+        med = statistics.median(times)
+        rows = kc.view(-1, 1024)[slots[:n_s].long()].cpu()
+        res["rows_bit_exact_vs_oracle"] = bool(torch.equal(rows, kc_c.view(-1, 1024)[sl.long()]))
+        res["cpu_baseline"] = dict(value=round(2 * 2 * n_s * 1024 * 2 / med / 1e9, 3), unit="GB/s",
+                                   cores=torch.get_num_threads(), kind="port",
+                                   sample=f"oracle store_kvcache (torch CPU, per-token loop), "
+                                          f"{n_s} tokens", seconds_per_sample=med)
+    return res
 
 
-def leg_prefill(torch, pkg, W, dev, steps, warmup):
+def leg_norm_rope(torch, pkg, dev, steps, warmup):
+    """Fused per-head QK-RMSNorm + RoPE + KV store (one call per layer in the
+    model) at a decode batch (256 tokens) and a prefill chunk (8,192 tokens):
+    reads the qkv row (8 KB per token), its position, slot and cos/sin row
+    (512 B), writes q (4 KB) and the K and V rows (2 KB each) of the token."""
+    from oracle import norm_rope as ON
+    from oracle import paged as OP
+    qmod = pkg.qwen3_naive
+    rope = qmod.RotaryEmbedding(128, 40960, 1000000.0)
+    cache = rope.cos_sin_cache.to(dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    qw = (1.0 + 0.1 * torch.randn(128, generator=g, device=dev)).to(torch.bfloat16)
+    kw = (1.0 + 0.1 * torch.randn(128, generator=g, device=dev)).to(torch.bfloat16)
+    out = {}
+    per_token = 4096 * 2 + 2048 * 2 + 2 * 1024 * 2 + 8 + 4 + 128 * 4
+    for name, n in (("decode_256", 256), ("prefill_8192", 8192)):
+        nb = n // 256 + 8
+        kc = torch.zeros((nb, 256, 8, 128), dtype=torch.bfloat16, device=dev)
+        vc = torch.zeros_like(kc)
+        qkv = torch.randn((n, 4096), generator=g, device=dev).to(torch.bfloat16)
+        pos = torch.randint(0, 4096, (n,), generator=g, device=dev)
+        gc = torch.Generator().manual_seed(n)
+        slots = torch.randperm(nb * 256, generator=gc)[:n].to(torch.int32).to(dev)
+        fn = lambda: pkg.kernels.qk_norm_rope_store(qkv, qw, kw, pos, cache, 16, 8, 1e-6, kc, vc,
+                                                    slots)
+        us = graph_us_per_call(torch, fn, steps, warmup)
+        _, per = timed_launches(torch, [fn], max(10, steps // 2), warmup)
+        q = fn()
+        torch.cuda.synchronize()
+        rec = dict(tokens=n, us_per_launch=round(us, 2),
+                   us_per_eager_call=round(statistics.median(per) * 1e3, 2),
+                   bytes_per_launch=per_token * n,
+                   gbs=round(per_token * n / (us * 1e-6) / 1e9, 1))
+        rec["frac_of_hbm_peak"] = round(rec["gbs"] / HBM_PEAK_GBS, 4)
+        if name == "prefill_8192":
+            # Oracle on the host: norm + rotate + store, fp32 math, bf16 results.
+            torch.set_num_threads(os.cpu_count() or 1)
+            qkv_c, pos_c, cache_c = qkv.cpu(), pos.cpu(), cache.cpu()
+            kc_c, vc_c = torch.zeros_like(kc, device="cpu"), torch.zeros_like(vc, device="cpu")
+
+            def cpu_step():
+                qh = ON.rms_norm(qkv_c[:, :2048].reshape(n, 16, 128), qw.cpu(), 1e-6)
+                kh = ON.rms_norm(qkv_c[:, 2048:3072].reshape(n, 8, 128), kw.cpu(), 1e-6)
+                qr = ON.apply_rope(qh, pos_c, cache_c)
+                kr = ON.apply_rope(kh, pos_c, cache_c)
+                OP.store_kvcache(kr, qkv_c[:, 3072:].reshape(n, 8, 128), kc_c, vc_c, slots.cpu())
+                return qr
+            times = []
+            for _ in range(3):
+                t = time.perf_counter()
+                q_ref = cpu_step()
+                times.append(time.perf_counter() - t)
+            med = statistics.median(times)
+            rec["max_abs_err_q_vs_oracle"] = (q.float().cpu() - q_ref.float()).abs().max().item()
+            rec["max_abs_err_k_rows_vs_oracle"] = (kc.float().cpu() - kc_c.float()).abs().max().item()
+            rec["v_rows_bit_exact"] = bool(torch.equal(vc.cpu(), vc_c))
+            rec["cpu_baseline"] = dict(value=round(per_token * n / med / 1e9, 3), unit="GB/s",
+                                       cores=torch.get_num_threads(), kind="port",
+                                       sample="oracle rms_norm + apply_rope + store_kvcache "
+                                              "(fp32 torch CPU, per-token store loop), 8,192 tokens",
+                                       seconds_per_sample=med)
+        out[name] = rec
+    return out
+
+
+def leg_host_prepare(torch, pkg, n_seqs=256, steps=200):
+    """Host-side decode step preparation (slot of the new token, -1-padded
+    page tables, ids, positions, context lengths) for 256 sequences of ~640
+    tokens (3 pages), as numpy arrays ready for one pinned copy; beside it the
+    oracle's per-sequence restatement of the reference's loops."""
+    from oracle import paged as OP
+    P = pkg.paged
+    rng = __import__("random").Random(0)
+    seqs, dicts = [], []
+    for i in range(n_seqs):
+        n_tok = 129 + rng.randrange(1024)
+        s = P.Sequence([rng.randrange(151936) for _ in range(n_tok)])
+        s.block_table = [rng.randrange(1362) for _ in range((n_tok + 255) // 256)]
+        s.kv_len = n_tok - 1
+        seqs.append(s)
+        dicts.append(dict(block_table=s.block_table, kv_len=s.kv_len))
+    P.prepare_decode(seqs)
+    t = time.perf_counter()
+    for _ in range(steps):
+        P.prepare_decode(seqs)
+    ours = (time.perf_counter() - t) / steps
+
+    def oracle_step():
+        slots = [OP.decode_slot(d["block_table"], d["kv_len"]) for d in dicts]
+        tables = OP.block_tables([d["block_table"] for d in dicts])
+        ids = [s.token_ids[-1] for s in seqs]
+        pos = [len(s.token_ids) - 1 for s in seqs]
+        ctx = [d["kv_len"] for d in dicts]
+        return torch.tensor(ids), torch.tensor(pos), torch.tensor(ctx, dtype=torch.int32), \
+            torch.tensor(tables, dtype=torch.int32), torch.tensor(slots, dtype=torch.int32)
+    oracle_step()
+    t = time.perf_counter()
+    for _ in range(steps):
+        oracle_step()
+    ref = (time.perf_counter() - t) / steps
+    got = P.prepare_decode(seqs)
+    want = oracle_step()
+    same = all(bool((torch.as_tensor(a).long() == b.long()).all()) for a, b in zip(got, want))
+    return dict(sequences=n_seqs, us_per_step=round(ours * 1e6, 1),
+                oracle_loop_us_per_step=round(ref * 1e6, 1), equal_to_oracle=same)
+
+
+def leg_prefill(torch, pkg, W, dev, steps, warmup, cpu=True):
     """Config 4: one layer's attention over every chunk step of the prefix-cache
     workload (16 sequences, 512-token shared prefix, suffixes U{256..2048} in
     512-token chunks).  Algorithmic FLOPs count unmasked (query, key) pairs."""
@@ -184,9 +333,37 @@ def leg_prefill(torch, pkg, W, dev, steps, warmup):
         c["max_seqlen_k"], 128 ** -0.5, True, c["block_tables"])) for c in calls]
     total_ms, per = timed_launches(torch, fns, steps, warmup)
     ms = total_ms / steps
-    return dict(ms_per_layer=ms, tflops=flops / (ms * 1e-3) / 1e12, flops=flops,
-                causal_pairs=pairs, n_steps=len(calls),
-                q_tokens=sum(int(c["cu_seqlens_q"][-1]) for c in calls))
+    res = dict(ms_per_layer=ms, tflops=flops / (ms * 1e-3) / 1e12, flops=flops,
+               causal_pairs=pairs, n_steps=len(calls),
+               q_tokens=sum(int(c["cu_seqlens_q"][-1]) for c in calls))
+    if cpu:
+        # The oracle (fp32 torch CPU) on the first two sequences of the first
+        # chunk step: 2 x 512 queries over 1,024 keys each.
+        from oracle import attention as OA
+        torch.set_num_threads(os.cpu_count() or 1)
+        c = calls[0]
+        cq = c["cu_seqlens_q"].cpu()[:3]
+        ck = c["cu_seqlens_k"].cpu()[:3]
+        nq = int(cq[-1])
+        q_c = c["q"][:nq].cpu()
+        bt_c = c["block_tables"][:2].cpu()
+        kc_c, vc_c = kc.cpu(), vc.cpu()
+        s_pairs = W.causal_pairs(cq.tolist(), ck.tolist())
+        times = []
+        for _ in range(2):
+            t = time.perf_counter()
+            ref = OA.varlen_prefill(q_c, kc_c, vc_c, cq, ck, bt_c, 128 ** -0.5)
+            times.append(time.perf_counter() - t)
+        med = statistics.median(times)
+        out = fns[0]()
+        torch.cuda.synchronize()
+        res["max_abs_err_vs_oracle"] = (out[:nq].float().cpu() - ref).abs().max().item()
+        res["cpu_baseline"] = dict(value=round(4 * 16 * 128 * s_pairs / med / 1e12, 4),
+                                   unit="TFLOP/s", cores=torch.get_num_threads(), kind="port",
+                                   sample="oracle varlen_prefill (fp32 torch CPU), first two "
+                                          "sequences of the first chunk step (2 x 512 queries)",
+                                   seconds_per_sample=med)
+    return res
 
 
 # ---------------------------------------------------------------------------
@@ -526,7 +703,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--legs", default="decode1,decode,grpo,store,prefill,rollout")
+    ap.add_argument("--legs", default="decode1,decode,grpo,store,prefill,norm_rope,host,rollout")
     ap.add_argument("--rollout-tokens", type=int, default=1024,
                     help="new tokens per sequence in the end-to-end rollout leg")
     ap.add_argument("--rollout-compare-tokens", type=int, default=64,
@@ -571,9 +748,14 @@ def main() -> int:
     if "grpo" in legs:
         results["grpo"] = leg_grpo(torch, pkg, W, dev, max(3, args.steps // 2), args.warmup)
     if "store" in legs:
-        results["store"] = leg_store(torch, pkg, dev, args.steps, args.warmup)
+        results["store"] = leg_store(torch, pkg, dev, args.steps, args.warmup, cpu=not args.no_cpu)
     if "prefill" in legs:
-        results["prefill"] = leg_prefill(torch, pkg, W, dev, max(3, args.steps // 2), args.warmup)
+        results["prefill"] = leg_prefill(torch, pkg, W, dev, max(3, args.steps // 2), args.warmup,
+                                         cpu=not args.no_cpu)
+    if "norm_rope" in legs:
+        results["norm_rope"] = leg_norm_rope(torch, pkg, dev, args.steps, args.warmup)
+    if "host" in legs:
+        results["host"] = leg_host_prepare(torch, pkg)
     if "rollout" in legs:
         results["rollout"] = leg_rollout(torch, pkg, dev, new_tokens=args.rollout_tokens,
                                          compare_tokens=args.rollout_compare_tokens)
@@ -606,6 +788,20 @@ def main() -> int:
             "us_per_launch": round(r["avg_launch_us"], 2), "gbs": round(r["gbs"], 1),
             "frac_of_hbm_peak": round(r["gbs"] / HBM_PEAK_GBS, 4),
             "bytes_per_launch": r["bytes_per_launch"]}
+        for k in ("rows_bit_exact_vs_oracle", "cpu_baseline"):
+            if k in r:
+                secondary["kv_store"][k] = r[k]
+
+    if "norm_rope" in results:
+        secondary["qk_norm_rope_store"] = {
+            "workload": "fused per-head QK-RMSNorm + RoPE + KV store, Hq 16 / Hkv 8, head_dim 128 "
+                        "(16,908 B per token: qkv row, position, slot and cos/sin row in; q, "
+                        "K and V rows out)", **results["norm_rope"]}
+
+    if "host" in results:
+        secondary["host_decode_prepare"] = {
+            "workload": "host-side decode step inputs (new-token slots, -1-padded page tables, "
+                        "ids, positions, context lengths) for 256 sequences", **results["host"]}
 
     if "decode1" in results:
         r = results["decode1"]
@@ -627,6 +823,9 @@ def main() -> int:
             "frac_of_bf16_mfma_peak": round(r["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4),
             "flops_per_layer": r["flops"], "causal_pairs": r["causal_pairs"],
             "chunk_steps": r["n_steps"], "query_tokens": r["q_tokens"]}
+        for k in ("max_abs_err_vs_oracle", "cpu_baseline"):
+            if k in r:
+                secondary["prefill_attention"][k] = r[k]
 
     if "rollout" in results:
         r = results["rollout"]

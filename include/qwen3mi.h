@@ -179,6 +179,9 @@ int qmi_add_rms_norm(const uint16_t* x, int64_t x_stride, const uint16_t* residu
  * (first 64 columns cos, last 64 sin) at positions[tok] (int64, clamped to
  * [0, max_position)).  Writes q_out [n_tok, Hq, 128] and k_out
  * [n_tok, Hkv, 128] (row strides q_stride / k_stride).  head_dim 128 only.
+ * Alignment (else QMI_E_BAD_STRIDE): qkv and cos_sin_cache 16-byte aligned
+ * with qkv_stride % 8 == 0; q_out, k_out and the weights 8-byte aligned with
+ * q_stride % 4 == 0 and k_stride % 4 == 0.
  */
 int qmi_qk_norm_rope(const uint16_t* qkv, int64_t qkv_stride, int64_t n_tok, int64_t num_q_heads,
                      int64_t num_kv_heads, int64_t head_dim, const uint16_t* q_norm_weight,
@@ -195,7 +198,8 @@ int qmi_qk_norm_rope(const uint16_t* qkv, int64_t qkv_stride, int64_t n_tok, int
  * slots outside [0, n_slots) are skipped.  Replaces q_norm / k_norm + RoPE +
  * store_kvcache(k, v, ...) in Qwen3Attention.forward_prefill
  * (qwen3_naive.py:611-626) and forward_decode (:655-668); results are
- * bit-identical to qmi_qk_norm_rope followed by qmi_store_kvcache.
+ * bit-identical to qmi_qk_norm_rope followed by qmi_store_kvcache.  Same
+ * alignment rules, and the caches 16-byte aligned.
  */
 int qmi_qk_norm_rope_store(const uint16_t* qkv, int64_t qkv_stride, int64_t n_tok,
                            int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,

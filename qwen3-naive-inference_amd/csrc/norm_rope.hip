@@ -96,10 +96,13 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_rows(
 
 // ---------------------------------------------------------------------------
 // Fused per-head RMSNorm + RoPE for q and k of a fused qkv row.
-// One wave64 per (token, head); lane j < 64 owns the RoPE pair (j, j + 64).
-// k goes to k_out (when given) and, with the caches given, the rotated k and
-// the token's v head go straight to cache row slots[tok] (slots outside
-// [0, n_slots) are skipped, as in the KV store).
+// 16 lanes per (token, head) item, four items per wave: lane s of an item owns
+// the RoPE pairs (4s + i, 64 + 4s + i), i < 4, read and written 8 bytes at a
+// time (cos / sin 16 bytes); the sum of squares stays inside the item's DPP
+// row of 16 lanes.  k goes to k_out (when given) and, with the caches given,
+// the rotated k and the token's v head (16 bytes per lane) go straight to
+// cache row slots[tok] (slots outside [0, n_slots) are skipped, as in the KV
+// store).
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     const uint16_t* __restrict__ qkv, int64_t qkv_stride, int n_q_heads, int n_kv_heads,
     const uint16_t* __restrict__ q_w, const uint16_t* __restrict__ k_w,
@@ -109,10 +112,10 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     uint16_t* __restrict__ v_cache, const int32_t* __restrict__ slots, int64_t n_slots,
     int64_t n_tok, float eps) {
   constexpr int D = 128, HALF = 64;
-  const int lane = threadIdx.x & 63;
-  const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int sub = threadIdx.x & 15;
+  const int64_t item = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
   const int heads = n_q_heads + n_kv_heads;
-  if (item >= n_tok * heads) return;
+  if (item >= n_tok * heads) return;  // whole 16-lane rows only
   const int64_t tok = item / heads;
   const int h = (int)(item - tok * heads);
   const bool is_q = h < n_q_heads;
@@ -121,42 +124,54 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
   int64_t pos = positions[tok];
   const uint16_t* src = qkv + tok * qkv_stride + (int64_t)h * D;
   const uint16_t* w = is_q ? q_w : k_w;
-  const float x1 = bf16_to_f32(src[lane]);
-  const float x2 = bf16_to_f32(src[lane + HALF]);
-  const float w1 = bf16_to_f32(w[lane]);
-  const float w2 = bf16_to_f32(w[lane + HALF]);
+  const uint2 xa = *reinterpret_cast<const uint2*>(src + 4 * sub);
+  const uint2 xb = *reinterpret_cast<const uint2*>(src + HALF + 4 * sub);
+  const uint2 wa = *reinterpret_cast<const uint2*>(w + 4 * sub);
+  const uint2 wb = *reinterpret_cast<const uint2*>(w + HALF + 4 * sub);
   pos = pos < 0 ? 0 : (pos >= max_pos ? max_pos - 1 : pos);
-  const float c = cos_sin[pos * D + lane];
-  const float s = cos_sin[pos * D + HALF + lane];
-  const float ss = wave_sum(x1 * x1 + x2 * x2);
+  const float4 c = *reinterpret_cast<const float4*>(cos_sin + pos * D + 4 * sub);
+  const float4 sn = *reinterpret_cast<const float4*>(cos_sin + pos * D + HALF + 4 * sub);
+  const float x1[4] = {bf16_lo(xa.x), bf16_hi(xa.x), bf16_lo(xa.y), bf16_hi(xa.y)};
+  const float x2[4] = {bf16_lo(xb.x), bf16_hi(xb.x), bf16_lo(xb.y), bf16_hi(xb.y)};
+  const float w1[4] = {bf16_lo(wa.x), bf16_hi(wa.x), bf16_lo(wa.y), bf16_hi(wa.y)};
+  const float w2[4] = {bf16_lo(wb.x), bf16_hi(wb.x), bf16_lo(wb.y), bf16_hi(wb.y)};
+  const float cc[4] = {c.x, c.y, c.z, c.w}, ss4[4] = {sn.x, sn.y, sn.z, sn.w};
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ss += x1[i] * x1[i] + x2[i] * x2[i];
+  ss = row16_sum(ss);
   const float inv = rsqrtf(ss / (float)D + eps);
-  // QK-norm output is bf16 in the reference before RoPE reads it.
-  const float n1 = bf16_to_f32(f32_to_bf16(x1 * inv * w1));
-  const float n2 = bf16_to_f32(f32_to_bf16(x2 * inv * w2));
-  const float o1 = n1 * c - n2 * s;
-  const float o2 = n2 * c + n1 * s;
-  const uint16_t b1 = f32_to_bf16(o1), b2 = f32_to_bf16(o2);
+  float o1[4], o2[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    // QK-norm output is bf16 in the reference before RoPE reads it.
+    const float n1 = bf16_to_f32(f32_to_bf16(x1[i] * inv * w1[i]));
+    const float n2 = bf16_to_f32(f32_to_bf16(x2[i] * inv * w2[i]));
+    o1[i] = n1 * cc[i] - n2 * ss4[i];
+    o2[i] = n2 * cc[i] + n1 * ss4[i];
+  }
+  const uint2 ba = make_uint2(pack_bf16x2(o1[0], o1[1]), pack_bf16x2(o1[2], o1[3]));
+  const uint2 bb = make_uint2(pack_bf16x2(o2[0], o2[1]), pack_bf16x2(o2[2], o2[3]));
   if (is_q) {
     uint16_t* dst = q_out + tok * q_stride + (int64_t)h * D;
-    dst[lane] = b1;
-    dst[lane + HALF] = b2;
+    *reinterpret_cast<uint2*>(dst + 4 * sub) = ba;
+    *reinterpret_cast<uint2*>(dst + HALF + 4 * sub) = bb;
     return;
   }
   const int hk = h - n_q_heads;
   if (k_out) {
     uint16_t* dst = k_out + tok * k_stride + (int64_t)hk * D;
-    dst[lane] = b1;
-    dst[lane + HALF] = b2;
+    *reinterpret_cast<uint2*>(dst + 4 * sub) = ba;
+    *reinterpret_cast<uint2*>(dst + HALF + 4 * sub) = bb;
   }
   if (k_cache) {
     const int64_t slot = slots[tok];
     if (slot >= 0 && slot < n_slots) {
       const int64_t row = slot * n_kv_heads * D + (int64_t)hk * D;
-      k_cache[row + lane] = b1;
-      k_cache[row + lane + HALF] = b2;
+      *reinterpret_cast<uint2*>(k_cache + row + 4 * sub) = ba;
+      *reinterpret_cast<uint2*>(k_cache + row + HALF + 4 * sub) = bb;
       const uint16_t* vsrc = qkv + tok * qkv_stride + (int64_t)(n_q_heads + n_kv_heads + hk) * D;
-      v_cache[row + lane] = vsrc[lane];
-      v_cache[row + lane + HALF] = vsrc[lane + HALF];
+      *reinterpret_cast<uint4*>(v_cache + row + 8 * sub) = *reinterpret_cast<const uint4*>(vsrc + 8 * sub);
     }
   }
 }
@@ -190,6 +205,7 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restric
 }
 
 inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline bool al8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
 
 }  // namespace
 
@@ -240,9 +256,12 @@ extern "C" int qmi_qk_norm_rope(const uint16_t* qkv, int64_t qkv_stride, int64_t
   if (qkv_stride < (num_q_heads + 2 * num_kv_heads) * head_dim || q_stride < num_q_heads * 128 ||
       k_stride < num_kv_heads * 128)
     return QMI_E_BAD_STRIDE;
+  if (qkv_stride % 8 || q_stride % 4 || k_stride % 4 || !al16(qkv) || !al8(q_out) || !al8(k_out) ||
+      !al16(cos_sin_cache) || !al8(q_norm_weight) || !al8(k_norm_weight))
+    return QMI_E_BAD_STRIDE;
   const int64_t items = n_tok * (num_q_heads + num_kv_heads);
-  if ((items + 3) / 4 > 0x7fffffffLL) return QMI_E_UNSUPPORTED;
-  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0,
+  if ((items + 15) / 16 > 0x7fffffffLL) return QMI_E_UNSUPPORTED;
+  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned)((items + 15) / 16)), dim3(256), 0,
                      reinterpret_cast<hipStream_t>(stream), qkv, qkv_stride, (int)num_q_heads,
                      (int)num_kv_heads, q_norm_weight, k_norm_weight, positions, cos_sin_cache,
                      max_position, q_out, q_stride, k_out, k_stride, nullptr, nullptr, nullptr,
@@ -266,9 +285,12 @@ extern "C" int qmi_qk_norm_rope_store(
   if (num_q_heads > 4096 || num_kv_heads > 4096) return QMI_E_UNSUPPORTED;
   if (qkv_stride < (num_q_heads + 2 * num_kv_heads) * head_dim || q_stride < num_q_heads * 128)
     return QMI_E_BAD_STRIDE;
+  if (qkv_stride % 8 || q_stride % 4 || !al16(qkv) || !al8(q_out) || !al16(cos_sin_cache) ||
+      !al8(q_norm_weight) || !al8(k_norm_weight) || !al16(k_cache) || !al16(v_cache))
+    return QMI_E_BAD_STRIDE;
   const int64_t items = n_tok * (num_q_heads + num_kv_heads);
-  if ((items + 3) / 4 > 0x7fffffffLL) return QMI_E_UNSUPPORTED;
-  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0,
+  if ((items + 15) / 16 > 0x7fffffffLL) return QMI_E_UNSUPPORTED;
+  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned)((items + 15) / 16)), dim3(256), 0,
                      reinterpret_cast<hipStream_t>(stream), qkv, qkv_stride, (int)num_q_heads,
                      (int)num_kv_heads, q_norm_weight, k_norm_weight, positions, cos_sin_cache,
                      max_position, q_out, q_stride, nullptr, (int64_t)0, k_cache, v_cache,
