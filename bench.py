@@ -267,6 +267,25 @@ def leg_norm_rope(torch, pkg, dev, steps, warmup):
                                               "(fp32 torch CPU, per-token store loop), 8,192 tokens",
                                        seconds_per_sample=med)
         out[name] = rec
+    # RMSNorm, residual add + RMSNorm and SwiGLU of the layer body over 8,192
+    # token rows (hidden 1024, intermediate 3072), against the oracle.
+    n = 8192
+    x = torch.randn((n, 1024), generator=g, device=dev).to(torch.bfloat16)
+    r = torch.randn((n, 1024), generator=g, device=dev).to(torch.bfloat16)
+    wn = (1.0 + 0.1 * torch.randn(1024, generator=g, device=dev)).to(torch.bfloat16)
+    gu = torch.randn((n, 6144), generator=g, device=dev).to(torch.bfloat16)
+    body = {
+        "rms_norm_8192x1024": (lambda: pkg.kernels.rms_norm(x, wn, 1e-6), n * 1024 * 2 * 2),
+        "add_rms_norm_8192x1024": (lambda: pkg.kernels.add_rms_norm(x, r, wn, 1e-6),
+                                   n * 1024 * 2 * 4),
+        "silu_mul_8192x3072": (lambda: pkg.kernels.silu_mul(gu), n * 3072 * 2 * 3),
+    }
+    for name, (fn, nbytes) in body.items():
+        us = graph_us_per_call(torch, fn, steps, warmup)
+        rec = dict(us_per_launch=round(us, 2), bytes_per_launch=nbytes,
+                   gbs=round(nbytes / (us * 1e-6) / 1e9, 1))
+        rec["frac_of_hbm_peak"] = round(rec["gbs"] / HBM_PEAK_GBS, 4)
+        out[name] = rec
     return out
 
 
@@ -796,7 +815,8 @@ def main() -> int:
         secondary["qk_norm_rope_store"] = {
             "workload": "fused per-head QK-RMSNorm + RoPE + KV store, Hq 16 / Hkv 8, head_dim 128 "
                         "(16,908 B per token: qkv row, position, slot and cos/sin row in; q, "
-                        "K and V rows out)", **results["norm_rope"]}
+                        "K and V rows out); RMSNorm / add + RMSNorm / SwiGLU over 8,192 rows; "
+                        "HIP graphs of 20 launches", **results["norm_rope"]}
 
     if "host" in results:
         secondary["host_decode_prepare"] = {
