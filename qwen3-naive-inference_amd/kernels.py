@@ -281,6 +281,8 @@ def qk_norm_rope(qkv: torch.Tensor, q_norm_weight: torch.Tensor, k_norm_weight: 
     _require_dtype("qkv", qkv, torch.bfloat16)
     if qkv.dim() != 2 or qkv.stride(1) != 1:
         raise ValueError("qkv must be a row-major [N, (Hq + 2 Hkv) * 128] tensor")
+    if qkv.data_ptr() % 16 or qkv.stride(0) % 8:
+        qkv = qkv.clone()  # the kernel reads rows 8 / 16 bytes at a time
     n = qkv.shape[0]
     pos = positions.reshape(-1)
     if pos.dtype != torch.int64:
@@ -316,6 +318,8 @@ def qk_norm_rope_store(qkv: torch.Tensor, q_norm_weight: torch.Tensor,
     _require_dtype("qkv", qkv, torch.bfloat16)
     if qkv.dim() != 2 or qkv.stride(1) != 1:
         raise ValueError("qkv must be a row-major [N, (Hq + 2 Hkv) * 128] tensor")
+    if qkv.data_ptr() % 16 or qkv.stride(0) % 8:
+        qkv = qkv.clone()  # the kernel reads rows 8 / 16 bytes at a time
     n = qkv.shape[0]
     pos = positions.reshape(-1)
     if pos.dtype != torch.int64:

@@ -104,3 +104,64 @@ def test_silu_mul(pkg, gpu):
     ref = (torch.nn.functional.silu(gf) * uf).to(torch.bfloat16)
     ok, bad, mx = ulp_close(out, ref, 1.0)
     assert ok, f"{bad} elements beyond 1 ulp (max diff {mx})"
+
+
+@pytest.mark.parametrize("n,hq,hkv", [(7, 16, 8), (5, 8, 4), (1, 16, 8), (3, 4, 4)])
+def test_qk_norm_rope_store_partial_workgroups(pkg, gpu, n, hq, hkv):
+    """Token x head counts that leave the last workgroup (16 heads) partly
+    empty; other GQA ratios; every token stored."""
+    g = torch.Generator().manual_seed(20 + n + hq)
+    nb = 2
+    qkv = (torch.randn(n, (hq + 2 * hkv) * 128, generator=g) * 2).to(torch.bfloat16)
+    qw = (torch.rand(128, generator=g) + 0.5).to(torch.bfloat16)
+    kw = (torch.rand(128, generator=g) + 0.5).to(torch.bfloat16)
+    pos = torch.randint(0, 40960, (n,), generator=g)
+    slots = torch.randperm(nb * 256, generator=g)[:n].to(torch.int32)
+    cache = NR.rope_cache(128, 40960, 1e6)
+    kc = torch.zeros(nb, 256, hkv, 128, dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    print(f"[norm] partial workgroups n={n} hq={hq} hkv={hkv}", flush=True)
+    kcg, vcg = kc.to(gpu), vc.to(gpu)
+    q = pkg.kernels.qk_norm_rope_store(qkv.to(gpu), qw.to(gpu), kw.to(gpu), pos.to(gpu),
+                                       cache.to(gpu), hq, hkv, 1e-6, kcg, vcg, slots.to(gpu))
+    torch.cuda.synchronize()
+    qn = NR.rms_norm(qkv[:, :hq * 128].view(n, hq, 128), qw, 1e-6)
+    kn = NR.rms_norm(qkv[:, hq * 128:(hq + hkv) * 128].view(n, hkv, 128), kw, 1e-6)
+    rq = NR.apply_rope(qn, pos, cache, torch.bfloat16)
+    rk = NR.apply_rope(kn, pos, cache, torch.bfloat16)
+    ok, bad, mx = ulp_close(q, rq, 2.0)
+    assert ok, f"q: {bad} elements beyond 2 ulp (max diff {mx})"
+    got_k = kcg.cpu().view(-1, hkv, 128)[slots.long()]
+    ok, bad, mx = ulp_close(got_k, rk, 2.0)
+    assert ok, f"k: {bad} elements beyond 2 ulp (max diff {mx})"
+    v = qkv[:, (hq + hkv) * 128:].view(n, hkv, 128)
+    assert torch.equal(vcg.cpu().view(-1, hkv, 128)[slots.long()], v)
+
+
+def test_qk_norm_rope_misaligned_rows(pkg, gpu):
+    """The kernel reads rows 8 / 16 bytes at a time: through the C ABI a qkv
+    view starting one element into its storage is rejected (not read
+    unaligned); the Python wrapper copies it and gives the aligned result."""
+    import ctypes
+    n, hq, hkv = 4, 16, 8
+    row = (hq + 2 * hkv) * 128
+    g = torch.Generator().manual_seed(30)
+    src = torch.randn(n, row, generator=g).to(torch.bfloat16).to(gpu)
+    big = torch.zeros(n * row + 8, dtype=torch.bfloat16, device=gpu)
+    big[1:1 + n * row].copy_(src.reshape(-1))
+    qkv = big[1:1 + n * row].view(n, row)
+    w = torch.ones(128, dtype=torch.bfloat16, device=gpu)
+    pos = torch.arange(n, dtype=torch.int64, device=gpu)
+    cache = NR.rope_cache(128, 64, 1e6).to(gpu)
+    print("[norm] misaligned qkv rows", flush=True)
+    q_ref, k_ref = pkg.kernels.qk_norm_rope(src, w, w, pos, cache, hq, hkv, 1e-6)
+    q, k = pkg.kernels.qk_norm_rope(qkv, w, w, pos, cache, hq, hkv, 1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(q, q_ref) and torch.equal(k, k_ref)
+    q_out = torch.empty(n, hq, 128, dtype=torch.bfloat16, device=gpu)
+    k_out = torch.empty(n, hkv, 128, dtype=torch.bfloat16, device=gpu)
+    st = pkg._lib.lib().qmi_qk_norm_rope(
+        qkv.data_ptr(), qkv.stride(0), n, hq, hkv, 128, w.data_ptr(), w.data_ptr(), pos.data_ptr(),
+        cache.data_ptr(), cache.shape[0], q_out.data_ptr(), q_out.stride(0), k_out.data_ptr(),
+        k_out.stride(0), 1e-6, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert st != 0
