@@ -168,10 +168,13 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     const int64_t slot = slots[tok];
     if (slot >= 0 && slot < n_slots) {
       const int64_t row = slot * n_kv_heads * D + (int64_t)hk * D;
-      *reinterpret_cast<uint2*>(k_cache + row + 4 * sub) = ba;
-      *reinterpret_cast<uint2*>(k_cache + row + HALF + 4 * sub) = bb;
+      // Cache rows are written non-temporally, as in the KV store.
+      typedef __attribute__((ext_vector_type(2))) unsigned int u32x2_t;
+      __builtin_nontemporal_store(u32x2_t{ba.x, ba.y}, reinterpret_cast<u32x2_t*>(k_cache + row + 4 * sub));
+      __builtin_nontemporal_store(u32x2_t{bb.x, bb.y}, reinterpret_cast<u32x2_t*>(k_cache + row + HALF + 4 * sub));
       const uint16_t* vsrc = qkv + tok * qkv_stride + (int64_t)(n_q_heads + n_kv_heads + hk) * D;
-      *reinterpret_cast<uint4*>(v_cache + row + 8 * sub) = *reinterpret_cast<const uint4*>(vsrc + 8 * sub);
+      __builtin_nontemporal_store(*reinterpret_cast<const u32x4_t*>(vsrc + 8 * sub),
+                                  reinterpret_cast<u32x4_t*>(v_cache + row + 8 * sub));
     }
   }
 }
