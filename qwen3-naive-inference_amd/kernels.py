@@ -115,8 +115,8 @@ def paged_decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
         raise ValueError(f"GQA ratio Hq/Hkv must be 1, 2, 4 or 8 (Hq={hq}, Hkv={hkv})")
     if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
         raise ValueError("caches must be contiguous")
-    if q.stride(2) != 1 or q.stride(0) % 8 or q.stride(1) % 8:
-        q = q.contiguous()
+    if q.stride(2) != 1 or q.stride(0) % 8 or q.stride(1) % 8 or q.data_ptr() % 16:
+        q = _dense16(q)
     seqlens = _as_i32("cache_seqlens", cache_seqlens)
     bt = _as_i32("block_table", block_table)
     if seqlens.dim() != 1 or seqlens.shape[0] != bsz:
@@ -192,8 +192,8 @@ def varlen_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: to
         raise ValueError(f"GQA ratio Hq/Hkv must be 1, 2 or 4 (Hq={hq}, Hkv={hkv})")
     if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
         raise ValueError("caches must be contiguous")
-    if q.stride(2) != 1 or q.stride(0) % 8 or q.stride(1) % 8:
-        q = q.contiguous()
+    if q.stride(2) != 1 or q.stride(0) % 8 or q.stride(1) % 8 or q.data_ptr() % 16:
+        q = _dense16(q)
     cq = _as_i32("cu_seqlens_q", cu_seqlens_q).contiguous()
     ck = _as_i32("cu_seqlens_k", cu_seqlens_k).contiguous()
     bt = _as_i32("block_table", block_table)
@@ -232,12 +232,21 @@ def varlen_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: to
 # ---------------------------------------------------------------------------
 # RMSNorm / QK-norm + RoPE / SwiGLU (qwen3_naive.py:44-80, :156-169, :695-702)
 # ---------------------------------------------------------------------------
+def _dense16(t: torch.Tensor) -> torch.Tensor:
+    """``t`` itself if contiguous and 16-byte aligned, else a contiguous copy
+    (a fresh allocation is aligned; ``contiguous()`` alone does not copy a
+    contiguous view that starts mid-row)."""
+    if not t.is_contiguous():
+        return t.contiguous()
+    return t.clone() if t.data_ptr() % 16 else t
+
+
 def _rows2d(name: str, x: torch.Tensor) -> torch.Tensor:
     _require_cuda(name, x)
     _require_dtype(name, x, torch.bfloat16)
     x2 = x.reshape(-1, x.shape[-1])
     if x2.stride(1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
-        x2 = x2.contiguous()
+        x2 = _dense16(x2)
     return x2
 
 
@@ -282,7 +291,7 @@ def qk_norm_rope(qkv: torch.Tensor, q_norm_weight: torch.Tensor, k_norm_weight: 
     if qkv.dim() != 2 or qkv.stride(1) != 1:
         raise ValueError("qkv must be a row-major [N, (Hq + 2 Hkv) * 128] tensor")
     if qkv.data_ptr() % 16 or qkv.stride(0) % 8:
-        qkv = qkv.clone()  # the kernel reads rows 8 / 16 bytes at a time
+        qkv = _dense16(qkv)  # the kernel reads rows 8 / 16 bytes at a time
     n = qkv.shape[0]
     pos = positions.reshape(-1)
     if pos.dtype != torch.int64:
@@ -319,7 +328,7 @@ def qk_norm_rope_store(qkv: torch.Tensor, q_norm_weight: torch.Tensor,
     if qkv.dim() != 2 or qkv.stride(1) != 1:
         raise ValueError("qkv must be a row-major [N, (Hq + 2 Hkv) * 128] tensor")
     if qkv.data_ptr() % 16 or qkv.stride(0) % 8:
-        qkv = qkv.clone()  # the kernel reads rows 8 / 16 bytes at a time
+        qkv = _dense16(qkv)  # the kernel reads rows 8 / 16 bytes at a time
     n = qkv.shape[0]
     pos = positions.reshape(-1)
     if pos.dtype != torch.int64:

@@ -200,3 +200,18 @@ def test_decode_more_than_1024_sequences_uses_split_schedule(pkg, gpu):
     out = _decode(pkg, gpu, w)
     torch.cuda.synchronize()
     _check(out, w)
+
+
+def test_decode_misaligned_q_view(pkg, gpu):
+    """q starting mid-allocation (not 16-byte aligned) is copied by the shim."""
+    w = _ragged(33, [40, 300, 700])
+    q = w["q"]
+    big = torch.zeros(q.numel() + 8, dtype=torch.bfloat16, device=gpu)
+    big[1:1 + q.numel()].copy_(q.reshape(-1).to(gpu))
+    qm = big[1:1 + q.numel()].view(q.shape)
+    print("[decode] misaligned q", flush=True)
+    out = pkg.kernels.paged_decode_attention(qm, w["k_cache"].to(gpu), w["v_cache"].to(gpu),
+                                             w["cache_seqlens"].to(gpu),
+                                             w["block_tables"].to(gpu), w["scale"])
+    torch.cuda.synchronize()
+    _check(out, w)

@@ -165,3 +165,20 @@ def test_qk_norm_rope_misaligned_rows(pkg, gpu):
         cache.data_ptr(), cache.shape[0], q_out.data_ptr(), q_out.stride(0), k_out.data_ptr(),
         k_out.stride(0), 1e-6, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
     assert st != 0
+
+
+def test_body_kernels_accept_misaligned_views(pkg, gpu):
+    """Rows starting mid-allocation (not 16-byte aligned) are copied by the
+    shims and give the same result as aligned rows."""
+    g = torch.Generator().manual_seed(31)
+    x = torch.randn(6, 1024, generator=g).to(torch.bfloat16).to(gpu)
+    w = (torch.rand(1024, generator=g) + 0.5).to(torch.bfloat16).to(gpu)
+    big = torch.zeros(6 * 1024 + 8, dtype=torch.bfloat16, device=gpu)
+    big[3:3 + 6 * 1024].copy_(x.reshape(-1))
+    xm = big[3:3 + 6 * 1024].view(6, 1024)
+    print("[norm] misaligned rows", flush=True)
+    assert torch.equal(pkg.kernels.rms_norm(xm, w, 1e-6), pkg.kernels.rms_norm(x, w, 1e-6))
+    gu = torch.randn(6, 2 * 1024, generator=g).to(torch.bfloat16).to(gpu)
+    big2 = torch.zeros(6 * 2048 + 8, dtype=torch.bfloat16, device=gpu)
+    big2[5:5 + 6 * 2048].copy_(gu.reshape(-1))
+    assert torch.equal(pkg.kernels.silu_mul(big2[5:5 + 6 * 2048].view(6, 2048)), pkg.kernels.silu_mul(gu))

@@ -338,3 +338,20 @@ def test_prefill_auto_split_long_prefix(pkg, gpu, lq, prefix, hq, hkv):
     _check(out, q, kc, vc, [0, lq], [0, L], bt)
     whole = _run_split(pkg, gpu, q, kc, vc, [0, lq], [0, L], bt, 1 << 20)
     assert (out.float() - whole.float()).abs().max().item() <= 1e-2
+
+
+def test_prefill_misaligned_q_view(pkg, gpu):
+    """q starting mid-allocation (not 16-byte aligned) is copied by the shim."""
+    L = 200
+    kc, vc, bt = _pool(80, [L])
+    g = torch.Generator().manual_seed(81)
+    q = torch.randn(L, 16, 128, generator=g).to(torch.bfloat16)
+    big = torch.zeros(q.numel() + 8, dtype=torch.bfloat16, device=gpu)
+    big[1:1 + q.numel()].copy_(q.reshape(-1).to(gpu))
+    qm = big[1:1 + q.numel()].view(q.shape)
+    cq = torch.tensor([0, L], dtype=torch.int32, device=gpu)
+    print("[prefill] misaligned q", flush=True)
+    out = pkg.kernels.varlen_prefill_attention(qm, kc.to(gpu), vc.to(gpu), cq, cq, L, L, SCALE,
+                                               True, bt.to(gpu))
+    torch.cuda.synchronize()
+    _check(out, q, kc, vc, [0, L], [0, L], bt)
