@@ -37,6 +37,15 @@ HIPCC_FLAGS = [
     f"-I{INCLUDE}",
 ]
 
+# Per-file additions.  The prefill kernel's score maxima are fmaxf chains over
+# MFMA results; with NaN-quieting semantics the compiler puts a canonicalising
+# v_max_f32 x, x, x in front of every operand, with relaxed NaN handling the
+# chains become v_max3_f32.  That kernel never produces a NaN score from
+# finite inputs (stale page rows are masked to -inf before any maximum).
+EXTRA_FLAGS = {
+    "varlen_prefill.hip": ["-fno-honor-nans"],
+}
+
 
 def hipcc_path() -> str:
     rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
@@ -55,7 +64,7 @@ def sources() -> list[Path]:
 
 def _compile(src: Path, verbose: bool) -> Path:
     obj = OBJ_DIR / (src.stem + ".o")
-    cmd = [hipcc_path(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc_path(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -20,14 +20,17 @@
 //     query l%16) is exactly the B-operand layout of the second product
 //     O^T = V^T P^T once two 16-key blocks are packed to bf16, so P never
 //     leaves registers.
-//   * K and V tiles are copied global -> LDS by the gfx950 direct loads
-//     (global_load_lds_dwordx4: a wave-wide instruction fills 1 KB of LDS,
-//     lane l at base + 16 l), so no registers or LDS stores stage them.
+//   * K and V tiles are staged through registers: each lane loads its
+//     16-byte chunks of the next tile from the page (8 per tile) while the
+//     current tile is computed, then writes them to LDS (ds_write_b128, a
+//     wave-wide write fills 1 KB, lane l at base + 16 l).
 //     Rows are 256 bytes (one KV head of a token) with the 16-byte chunks
 //     XOR-swizzled instead of padded: chunk c of K row r sits at c ^ (r % 16)
 //     (16 consecutive rows then hit 16 distinct 4-bank groups for the A
-//     operand reads), chunk c of V row r at c ^ 2 (r % 4); each lane fetches
-//     the logical chunk that its physical slot holds.
+//     operand reads), chunk c of V row r at c ^ (2 (r % 4) + 8 ((r / 4) % 2))
+//     (the 8 rows that the two 16-lane groups of a transpose read's 32-lane
+//     half address then cover all 64 banks); each lane fetches the logical
+//     chunk that its physical slot holds.
 //   * The V^T operand is read with gfx950's LDS transpose read
 //     (ds_read_b64_tr_b16): in a 16-lane group, lane r receives 16-bit
 //     element r % 4 of lane 4e + r / 4's 8 bytes as element e, so pointing
@@ -35,17 +38,18 @@
 //     kbase .. kbase+3 of dim 16 db + r.  Two such reads (keys 32c + 4g and
 //     32c + 16 + 4g) form the 8 keys the B operand P^T packs for the lane.
 //     These reads are issued as inline asm with explicit LDS-counter waits,
-//     one 16-dim block ahead: the compiler would otherwise wait for every
-//     outstanding direct load (the next tile's) before the first of them.
+//     one 16-dim block ahead, with immediate offsets from per-lane bases
+//     fixed for the whole loop.
 //   * Online softmax in fp32 (log2 domain); per query the 4 lanes holding
 //     its keys agree on the running max through two VALU lane swaps.  The running
 //     sum of P is one more MFMA per 32 keys (A = a 16 x 32 block whose row 0
 //     is all ones), so it sums exactly the bf16 P the O^T product uses and
 //     costs no VALU adds.
 //   * K / V tiles of 64 keys (one quarter page) are double-buffered in LDS:
-//     the direct loads of tile t+1 are in flight while tile t is computed.
+//     the global loads of tile t+1 are in flight while tile t is computed,
+//     and their LDS writes go to the buffer no wave reads during tile t.
 //     Keys past the workgroup's last visible key are stale page rows: their
-//     scores are masked and their V rows zeroed once the tile has landed.
+//     scores are masked and their V rows are written to LDS as zeros.
 //   * Grid = (Hkv, B, query blocks): with 8 KV heads the KV head maps to the
 //     XCD, so all query blocks of one (sequence, KV head) share an L2.
 //     Query blocks are the slowest grid dimension and are issued last-first:
@@ -60,6 +64,7 @@
 //     row sum (fp32) to a workspace, and varlen_prefill_merge combines them;
 //     items that are not split write their output directly.
 #include <algorithm>
+#include <type_traits>
 
 #include "qmi_common.h"
 
@@ -74,6 +79,33 @@ constexpr int kKeyTile = 64;
 constexpr int kWaveQ = 32;              // queries per wave (two MFMA column blocks)
 typedef __attribute__((ext_vector_type(4))) short v4s_t;
 typedef __attribute__((ext_vector_type(2))) unsigned int v2u_t;
+
+// LDS transpose read (ds_read_b64_tr_b16) at a per-lane address plus an
+// immediate byte offset.  Issued as inline asm so that the compiler does not
+// put a wait for every outstanding memory operation in front of it; the
+// caller waits with lgkm_wait.
+template <int OFF>
+__device__ __forceinline__ v2u_t ds_read_tr16_b64(uint32_t addr) {
+  v2u_t r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF) : "memory");
+  return r;
+}
+
+// Waits until at most N LDS reads are outstanding; the four registers are
+// tied to the wait so that no use of them is scheduled above it.
+template <int N>
+__device__ __forceinline__ void lgkm_wait(v2u_t& a, v2u_t& b, v2u_t& c, v2u_t& d) {
+  asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "i"(N) : "memory");
+}
+
+// Calls f(std::integral_constant<int, i>) for i = I .. N-1.
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
   return __builtin_bit_cast(bf16x8_t, u32x4_t{v.x, v.y, v.z, v.w});
@@ -176,46 +208,88 @@ void varlen_prefill_kernel(
   // zeroed.  A tile whose page-table entry is outside [0, num_blocks) is
   // skipped in the compute.
   const int64_t row_elems = (int64_t)num_kv_heads * kHeadDim;
-  // Direct global -> LDS loads: wave w's instruction i fills rows 4q .. 4q+3
-  // (q = 4w + i) of a tile, lane l writing 16 bytes at row 4q + l / 16,
-  // physical chunk l % 16, fetched from the logical chunk the swizzle maps there.
+  // Tiles are staged through registers: at the start of tile t every lane
+  // loads its 16-byte chunks of tile t+1 (4 of K, 4 of V) into registers, and
+  // after tile t's compute writes them to the other LDS buffer.  (The gfx950
+  // direct global -> LDS loads cost ~30% of this kernel's time: their LDS
+  // writes hold up the waves' own LDS traffic, while the same bytes through
+  // registers and ds_write_b128 cost no measurable time.)  Chunk i of wave w
+  // covers rows 4q .. 4q+3 (q = 4w + i): lane l holds row 4q + l / 16,
+  // physical chunk l % 16 (fetched from the logical chunk the swizzle maps
+  // there) and writes it at byte 1024 q + 16 l of the buffer.
   uint32_t k_src[4], v_src[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = 4 * (4 * wave + i) + (lane >> 4), pc = lane & 15;
     k_src[i] = (uint32_t)((row * row_elems + 8 * (pc ^ (row & 15))) * 2);
-    v_src[i] = (uint32_t)((row * row_elems + 8 * (pc ^ ((row & 3) << 1))) * 2);
+    v_src[i] = (uint32_t)((row * row_elems + 8 * (pc ^ (((row & 3) << 1) | (row & 4) << 1))) * 2);
   }
+  // Page-table entries of the current segment of tiles, one per lane: lane i
+  // holds the entry of page pg0 + i (-1 past the table's width), read with
+  // v_readlane, so the tile loop has no memory load besides the tile's own.
+  int pg0 = 0, pg_lane = -1;
+  uint4 stg_k[4], stg_v[4];
   bool tile_ok[2] = {false, false};
   int st_valid[2] = {0, 0};
   auto load_tile = [&](int t, int buf) {
     const int key0 = t * kKeyTile;
-    const int32_t blk = block_table[(int64_t)b * bt_stride + key0 / kPage];
+    const int32_t blk = __builtin_amdgcn_readlane(pg_lane, key0 / kPage - pg0);
     const bool page_ok = blk >= 0 && blk < num_blocks;
     const int64_t row0 = (int64_t)(page_ok ? blk : 0) * kPage + (key0 % kPage);
     const char* kb = reinterpret_cast<const char*>(k_cache + row0 * row_elems + kvh * kHeadDim);
     const char* vb = reinterpret_cast<const char*>(v_cache + row0 * row_elems + kvh * kHeadDim);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int q4 = 4 * wave + i;
-      __builtin_amdgcn_global_load_lds(kb + k_src[i],
-          (__attribute__((address_space(3))) void*)&sK[buf][q4 * 4 * kHeadDim], 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(vb + v_src[i],
-          (__attribute__((address_space(3))) void*)&sV[buf][q4 * 4 * kHeadDim], 16, 0, 0);
+      stg_k[i] = load_u4(kb + k_src[i]);
+      stg_v[i] = load_u4(vb + v_src[i]);
     }
     st_valid[buf] = page_ok ? min(kKeyTile, kend - key0) : 0;
     tile_ok[buf] = st_valid[buf] > 0;
   };
-  // After the tile's loads have landed (every lane waited, then a barrier):
-  // zero V rows past the valid keys (0 * stale NaN would poison O).
-  auto fix_tile = [&](int buf) {
-    if (st_valid[buf] < kKeyTile) {
-      for (int c = tid; c < kKeyTile * 16; c += kThreads)
-        if ((c >> 4) >= st_valid[buf])
-          *reinterpret_cast<uint4*>(&sV[buf][(c >> 4) * kHeadDim + 8 * (c & 15)]) = make_uint4(0, 0, 0, 0);
-      __syncthreads();
+  // Writes the staged tile to LDS buffer buf.  V rows past the valid keys are
+  // written as zeros (0 * a stale NaN would poison O); stale K rows are masked
+  // in the scores.
+  auto store_tile = [&](int buf) {
+    const int valid = st_valid[buf];
+    if (valid < kKeyTile) {  // wave-uniform: partial tiles only
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = 4 * (4 * wave + i) + (lane >> 4);
+        if (row >= valid) stg_v[i] = make_uint4(0, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int q4 = 4 * wave + i;
+      *reinterpret_cast<uint4*>(&sK[buf][q4 * 4 * kHeadDim + 8 * lane]) = stg_k[i];
+      *reinterpret_cast<uint4*>(&sV[buf][q4 * 4 * kHeadDim + 8 * lane]) = stg_v[i];
     }
   };
+
+  // LDS operand addresses: per-lane bases fixed for the whole loop, with the
+  // buffer, key block, dim block and key half as immediate offsets (the tile
+  // loop is unrolled by buffer), so no address arithmetic is left per tile.
+  // K operand of key block kb, dim slice c: row 16 kb + l16, logical chunk
+  // 4c + g4, stored at physical chunk (4c + g4) ^ l16.
+  uint32_t k_lane[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) k_lane[c] = (uint32_t)(l16 * kHeadDim * 2 + 16 * ((4 * c + g4) ^ l16));
+  // V^T transpose reads of dim block db, key half c: lane i points at row
+  // R = 32c + 4 g4 + l16 / 4 (+16 for the second read), logical 8-byte piece
+  // 4 db + l16 % 4, i.e. chunk 2 db + x with x = (l16 % 4) / 2, stored at
+  // chunk (2 db + x) ^ (2 (R % 4) + 8 ((R / 4) % 2)) = 2 (db ^ w) + x with
+  // w = (l16 / 4) % 4 + 4 (g4 % 2): byte 32 (db ^ w) + 16 x + 8 (l16 % 2) of
+  // the row.  v_lane[db] holds that address for key half 0 of buffer 0.
+  uint32_t v_lane[8];
+  {
+    const uint32_t sv0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)&sV[0][0];
+    const int vrow = 4 * g4 + (l16 >> 2);
+    const int vx = (l16 & 3) >> 1, w = ((l16 >> 2) & 3) + 4 * (g4 & 1);
+#pragma unroll
+    for (int d = 0; d < 8; ++d)
+      v_lane[d] = sv0 + (uint32_t)(vrow * kHeadDim * 2 + 8 * (l16 & 1) + 16 * vx + 32 * (d ^ w));
+  }
+  const char* sk_bytes = reinterpret_cast<const char*>(&sK[0][0]);
 
   float m_run[2] = {kNegBig, kNegBig};  // running max (log2 domain) per query
   f32x4_t acc_l[2];                     // row 0 (lanes 0-15): running sum of P (bf16) per query
@@ -226,15 +300,15 @@ void varlen_prefill_kernel(
 #pragma unroll
     for (int db = 0; db < 8; ++db) acc_o[j][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  if (t_begin < t_end) load_tile(t_begin, 0);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (t_begin < t_end) fix_tile(0);
-
-  for (int t = t_begin; t < t_end; ++t) {
-    const int buf = (t - t_begin) & 1;
+  // One tile: tile t sits in LDS buffer BUF (a compile-time constant).  The
+  // next tile's loads are issued on every step (the last tile of a segment
+  // reloads itself into the idle buffer), so every path through the loop
+  // leaves the same loads outstanding and the compiler's waits stay at the
+  // LDS writes instead of moving to the top of the tile.
+  auto tile_step = [&](int t, int t_last, auto buf_c) __attribute__((always_inline)) {
+    constexpr int buf = decltype(buf_c)::value;
     const bool compute = tile_ok[buf];  // wave-uniform
-    if (t + 1 < t_end) load_tile(t + 1, buf ^ 1);
+    load_tile(min(t + 1, t_last), buf ^ 1);
     if (compute) {
 
     // ---- S^T = K Q^T for 4 blocks of 16 keys x 2 blocks of 16 queries ----
@@ -245,10 +319,9 @@ void varlen_prefill_kernel(
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) s[j][kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    // row 16 kb + l16, logical chunk 4c + g4 -> physical (4c + g4) ^ l16
-    const uint16_t* kbase = &sK[buf][l16 * kHeadDim];
     auto kchunk = [&](int kb, int c) {
-      return as_bf16x8(*reinterpret_cast<const uint4*>(kbase + kb * 16 * kHeadDim + 8 * ((4 * c + g4) ^ l16)));
+      return as_bf16x8(*reinterpret_cast<const uint4*>(sk_bytes + buf * kKeyTile * kHeadDim * 2 +
+                                                        kb * 16 * kHeadDim * 2 + k_lane[c]));
     };
     bf16x8_t kop[2][4];
 #pragma unroll
@@ -281,20 +354,24 @@ void varlen_prefill_kernel(
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       if (!full) {
+        // key = key_base + 16 kb + 4 g4 + r is visible iff key <= min(my_pos, Lk - 1).
+        const int lim = min(my_pos[j], Lk - 1) - key_base - 4 * g4;
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int key = key_base + kb * 16 + 4 * g4 + r;
-            const bool ok = key <= my_pos[j] && key < Lk;
-            s[j][kb][r] = ok ? s[j][kb][r] : -INFINITY;
-          }
+          for (int r = 0; r < 4; ++r)
+            s[j][kb][r] = 16 * kb + r <= lim ? s[j][kb][r] : -INFINITY;
         }
       }
-      float tmax = fmaxf(fmaxf(s[j][0][0], s[j][0][1]), fmaxf(s[j][0][2], s[j][0][3]));
-#pragma unroll
-      for (int kb = 1; kb < 4; ++kb)
-        tmax = fmaxf(tmax, fmaxf(fmaxf(s[j][kb][0], s[j][kb][1]), fmaxf(s[j][kb][2], s[j][kb][3])));
+      // Chained so that each pair of maxima is one v_max3_f32.
+      float tmax = fmaxf(fmaxf(s[j][0][0], s[j][0][1]), s[j][0][2]);
+      tmax = fmaxf(fmaxf(tmax, s[j][0][3]), s[j][1][0]);
+      tmax = fmaxf(fmaxf(tmax, s[j][1][1]), s[j][1][2]);
+      tmax = fmaxf(fmaxf(tmax, s[j][1][3]), s[j][2][0]);
+      tmax = fmaxf(fmaxf(tmax, s[j][2][1]), s[j][2][2]);
+      tmax = fmaxf(fmaxf(tmax, s[j][2][3]), s[j][3][0]);
+      tmax = fmaxf(fmaxf(tmax, s[j][3][1]), s[j][3][2]);
+      tmax = fmaxf(tmax, s[j][3][3]);
       tmax = rows4_max(tmax);
       const float m_cand = tmax * scale_log2;
       const bool need = m_cand > m_run[j] + 8.f;
@@ -323,33 +400,27 @@ void varlen_prefill_kernel(
 
     // ---- O^T += V^T P^T: V^T operands by LDS transpose reads ----
     // Issued as inline asm with explicit LDS-counter waits, so the reads of
-    // tile t do not wait for the direct loads of tile t+1 (still in flight).
+    // tile t do not wait for the global loads of tile t+1 (still in flight).
     {
-      const int vrow = 4 * g4 + (l16 >> 2);
-      const int vsw = ((l16 >> 2) & 3) << 1;
-      const uint32_t vb0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)&sV[buf][vrow * kHeadDim] + 8 * (l16 & 1);
-      auto vaddr = [&](int db, int c) -> uint32_t {
-        const int lc = 2 * db + ((l16 & 3) >> 1);
-        return vb0 + (uint32_t)(c * 32 * kHeadDim * 2 + 16 * (lc ^ vsw));
-      };
       v2u_t r[2][2][2];  // [stage][c][lo/hi]
-      auto issue = [&](int db, int st) {
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const uint32_t ad = vaddr(db, c);
-          asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r[st][c][0]) : "v"(ad) : "memory");
-          asm volatile("ds_read_b64_tr_b16 %0, %1 offset:4096" : "=v"(r[st][c][1]) : "v"(ad) : "memory");
-        }
+      auto issue = [&](auto db_c) __attribute__((always_inline)) {
+        constexpr int db = decltype(db_c)::value, st = db & 1;
+        constexpr int off0 = buf * kKeyTile * kHeadDim * 2;
+        constexpr int off1 = off0 + 32 * kHeadDim * 2;  // keys 32 .. 63
+        const uint32_t ad = v_lane[db];
+        r[st][0][0] = ds_read_tr16_b64<off0>(ad);
+        r[st][0][1] = ds_read_tr16_b64<off0 + 4096>(ad);
+        r[st][1][0] = ds_read_tr16_b64<off1>(ad);
+        r[st][1][1] = ds_read_tr16_b64<off1 + 4096>(ad);
       };
-      issue(0, 0);
-#pragma unroll
-      for (int db = 0; db < 8; ++db) {
-        const int st = db & 1;
-        if (db + 1 < 8) {
-          issue(db + 1, st ^ 1);
-          asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(r[st][0][0]), "+v"(r[st][0][1]), "+v"(r[st][1][0]), "+v"(r[st][1][1]) :: "memory");
+      issue(std::integral_constant<int, 0>{});
+      static_for<0, 8>([&](auto db_c) __attribute__((always_inline)) {
+        constexpr int db = decltype(db_c)::value, st = db & 1;
+        if constexpr (db + 1 < 8) {
+          issue(std::integral_constant<int, db + 1>{});
+          lgkm_wait<4>(r[st][0][0], r[st][0][1], r[st][1][0], r[st][1][1]);
         } else {
-          asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[st][0][0]), "+v"(r[st][0][1]), "+v"(r[st][1][0]), "+v"(r[st][1][1]) :: "memory");
+          lgkm_wait<0>(r[st][0][0], r[st][0][1], r[st][1][0], r[st][1][1]);
         }
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
@@ -359,7 +430,7 @@ void varlen_prefill_kernel(
           for (int j = 0; j < 2; ++j)
             acc_o[j][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[j][c], acc_o[j][db], 0, 0, 0);
         }
-      }
+      });
     }
       // Row sums of P by MFMA: A = 16 x 32 with row 0 all ones.
       {
@@ -372,9 +443,23 @@ void varlen_prefill_kernel(
             acc_l[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pop[j][c], acc_l[j], 0, 0, 0);
       }
     }  // compute
-    __builtin_amdgcn_s_waitcnt(0);
+    store_tile(buf ^ 1);
     __syncthreads();
-    if (t + 1 < t_end) fix_tile(buf ^ 1);
+  };
+  // Segments of at most kSegTiles tiles span at most 61 pages, within the 64
+  // lanes' page-table entries.
+  constexpr int kSegTiles = 240;
+  for (int seg = t_begin; seg < t_end; seg += kSegTiles) {
+    const int seg_last = min(t_end, seg + kSegTiles) - 1;
+    pg0 = seg * kKeyTile / kPage;
+    pg_lane = pg0 + lane < bt_width ? block_table[(int64_t)b * bt_stride + pg0 + lane] : -1;
+    load_tile(seg, 0);
+    store_tile(0);
+    __syncthreads();
+    for (int t = seg; t <= seg_last; t += 2) {
+      tile_step(t, seg_last, std::integral_constant<int, 0>{});
+      if (t + 1 <= seg_last) tile_step(t + 1, seg_last, std::integral_constant<int, 1>{});
+    }
   }
 
   if (item.n_parts > 1) {
