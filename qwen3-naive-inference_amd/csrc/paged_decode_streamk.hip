@@ -27,6 +27,19 @@
 // otherwise the segment's (acc, m, l) go to one of the workgroup's two
 // partial slots (its first and its last segment) and the merge kernel
 // combines the slots of the workgroups that shared the sequence.
+//
+// Head-group units.  For batches of 128 or more sequences the work unit is a
+// (sequence, group of HG KV heads) pair instead of a whole sequence, with HG
+// the fewest heads that still give two units per workgroup slot of the GPU
+// (4 of 8 heads at 256 sequences).  When the units are of nearly equal length
+// (a GRPO rollout: every sequence has the same prompt length and decodes in
+// lockstep), each workgroup takes exactly one whole unit ("unit mode"): no
+// sequence boundary inside a workgroup, no partial slots and nothing to merge.
+// Every workgroup takes that decision from the same scan of the context
+// lengths (unit mode iff the longest unit is at most 10% above the balanced
+// share of a workgroup), so it needs no host knowledge of the lengths and
+// holds inside a captured graph; otherwise the balanced split runs over the
+// units.
 #include "qmi_common.h"
 
 namespace {
@@ -37,9 +50,9 @@ constexpr int kHeadDim = 128;
 constexpr int kPage = 256;
 constexpr int kThreads = 256;
 constexpr int kTok = 4;                        // tokens per lane per step
-// A workgroup of 256 lanes covers 16 lanes x HKV heads per token group.
-template <int HKV> constexpr int kTokGroups = 16 / HKV;
-template <int HKV> constexpr int kStepTokens = kTokGroups<HKV> * kTok;   // divides the page
+// A workgroup of 256 lanes covers 16 lanes x HG heads per token group.
+template <int HG> constexpr int kTokGroups = 16 / HG;
+template <int HG> constexpr int kStepTokens = kTokGroups<HG> * kTok;   // divides the page
 constexpr int kSlotStride = kHeadDim + 4;      // acc[128], m, l, pad (per q head)
 constexpr int kMaxSeqScan = 1024;              // batch limit of the in-LDS prefix scan
 
@@ -65,24 +78,28 @@ __device__ __forceinline__ int64_t owner_of(int64_t s, int64_t total, int64_t n_
   return w < n_wg - 1 ? w : n_wg - 1;
 }
 
-// Prefix sum of per-sequence step counts into LDS (exclusive; off[B] = total).
+// Prefix sum of per-sequence step counts (steps of one unit of the sequence)
+// into LDS (exclusive; off[B] = total), and the largest count into *max_steps.
 // Each lane takes ceil(B / THREADS) consecutive sequences; lane sums are scanned
 // inside each wave with shuffles and across waves through LDS.
 template <int THREADS, int TS>
 __device__ void scan_steps(const int32_t* __restrict__ seqlens, int seqlen_bias, int bt_width,
-                           int batch, int* off) {
+                           int batch, int* off, int* max_steps) {
   __shared__ int wave_tot[THREADS / 64];
+  __shared__ int wave_max[THREADS / 64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int per = (batch + THREADS - 1) / THREADS;
   const int b0 = tid * per;
-  int mine = 0;
+  int mine = 0, mx = 0;
   for (int i = 0; i < per; ++i) {
     const int b = b0 + i;
     if (b < batch) {
       int L = seqlens[b] + seqlen_bias;
       L = max(0, min(L, bt_width * kPage));
       off[b] = mine;
-      mine += (L + TS - 1) / TS;
+      const int steps = (L + TS - 1) / TS;
+      mine += steps;
+      mx = max(mx, steps);
     }
   }
   int incl = mine;
@@ -90,78 +107,115 @@ __device__ void scan_steps(const int32_t* __restrict__ seqlens, int seqlen_bias,
   for (int d = 1; d < 64; d <<= 1) {
     const int t = __shfl_up(incl, d, 64);
     if (lane >= d) incl += t;
+    mx = max(mx, __shfl_xor(mx, d, 64));
   }
   if (lane == 63) wave_tot[wave] = incl;
+  if (lane == 0) wave_max[wave] = mx;
   __syncthreads();
   int base = incl - mine;
-  int total = 0;
+  int total = 0, all_max = 0;
 #pragma unroll
   for (int wv = 0; wv < THREADS / 64; ++wv) {
     if (wv < wave) base += wave_tot[wv];
     total += wave_tot[wv];
+    all_max = max(all_max, wave_max[wv]);
   }
   for (int i = 0; i < per; ++i) {
     const int b = b0 + i;
     if (b < batch) off[b] += base;
   }
-  if (tid == 0) off[batch] = total;
+  if (tid == 0) {
+    off[batch] = total;
+    *max_steps = all_max;
+  }
   __syncthreads();
 }
 
-template <int HKV, int G>
+// Unit mode: every unit is a whole workgroup's work when the longest unit is
+// at most 10% above the balanced share (and there is a workgroup per unit).
+__device__ __forceinline__ bool use_unit_mode(int64_t total, int max_steps, int64_t n_units,
+                                              int64_t n_wg_grid, int64_t n_bal) {
+  if (total == 0 || n_units > n_wg_grid) return false;
+  const int64_t n_act = active_wgs(total, n_bal);
+  const int64_t share = (total + n_act - 1) / n_act;
+  return (int64_t)max_steps * 10 <= share * 11;
+}
+
+// Grid: max(n_bal, units) workgroups.  n_bal = the balanced split's workgroup
+// count (two per CU), which also indexes the partial slots; the step offsets
+// and the mode word follow the slots of n_bal workgroups.
+template <int HKV, int G, int HG>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(G <= 2 ? 4 : 2)))
 void decode_streamk_split(
     const uint16_t* __restrict__ q, int64_t q_seq_stride, int64_t q_head_stride,
     const uint16_t* __restrict__ k_cache, const uint16_t* __restrict__ v_cache,
     int64_t num_blocks, const int32_t* __restrict__ seqlens, int seqlen_bias,
     const int32_t* __restrict__ block_table, int64_t bt_stride, int bt_width, int batch,
-    int n_wg, float scale_log2, uint16_t* __restrict__ out, int64_t out_seq_stride,
+    int n_bal, float scale_log2, uint16_t* __restrict__ out, int64_t out_seq_stride,
     int64_t out_head_stride, float* __restrict__ ws) {
-  constexpr int TG = kTokGroups<HKV>;
-  constexpr int TS = kStepTokens<HKV>;
+  constexpr int NHG = HKV / HG;                          // units (head groups) per sequence
+  constexpr int TG = kTokGroups<HG>;
+  constexpr int TS = kStepTokens<HG>;
   constexpr int HQ = HKV * G;
+  constexpr int GQ = HG * G;                             // query heads of a unit
   constexpr int kRowBytes = HKV * kHeadDim * 2;          // one token of every KV head
   constexpr int64_t kPageElems = (int64_t)kPage * HKV * kHeadDim;
   __shared__ int off[kMaxSeqScan + 1];
-  __shared__ float sm_acc[TG][HKV][G][kHeadDim];
-  __shared__ float sm_ml[TG][HKV][G][2];
+  __shared__ int sm_max_steps;
+  __shared__ float sm_acc[TG][HG][G][kHeadDim];
+  __shared__ float sm_ml[TG][HG][G][2];
 
   const int tid = threadIdx.x;
   const int lane16 = tid & 15;
-  const int h = (tid >> 4) % HKV;
-  const int tg = tid / (16 * HKV);
+  const int hl = (tid >> 4) % HG;                        // head within the unit's group
+  const int tg = tid / (16 * HG);
   const int64_t w = blockIdx.x;
-  // Byte offset of this lane's 16 B inside a step: token group tg owns the
-  // kTok consecutive tokens [tg*kTok, +kTok) of the step.
-  const uint32_t lane_off = (uint32_t)(tg * kTok * kRowBytes + (h * kHeadDim + lane16 * 8) * 2);
 
-  scan_steps<kThreads, TS>(seqlens, seqlen_bias, bt_width, batch, off);
-  if (w == 0) {  // publish the step offsets for the merge kernel
-    int32_t* ws_off = reinterpret_cast<int32_t*>(ws + (int64_t)n_wg * 2 * HQ * kSlotStride);
+  scan_steps<kThreads, TS>(seqlens, seqlen_bias, bt_width, batch, off, &sm_max_steps);
+  const int64_t total = (int64_t)NHG * off[batch];      // unit steps of the launch
+  const int64_t n_units = (int64_t)batch * NHG;
+  const bool unit_mode = use_unit_mode(total, sm_max_steps, n_units, gridDim.x, n_bal);
+  if (w == 0) {  // publish the step offsets and the mode for the merge kernel
+    int32_t* ws_off = reinterpret_cast<int32_t*>(ws + (int64_t)n_bal * 2 * HQ * kSlotStride);
     for (int i = tid; i <= batch; i += kThreads) ws_off[i] = off[i];
+    if (tid == 0) ws_off[batch + 1] = unit_mode ? 1 : 0;
   }
-  const int64_t total = off[batch];
   if (total == 0) return;
-  const int64_t n_act = active_wgs(total, n_wg);
-  if (w >= n_act) return;
-  const int64_t s_begin = range_start(w, total, n_act);
-  const int64_t s_end = range_start(w + 1, total, n_act);
+  int64_t s_begin, s_end;
+  if (unit_mode) {  // one whole unit per workgroup
+    if (w >= n_units) return;
+    const int ub = (int)(w / NHG);
+    const int64_t steps_b = off[ub + 1] - off[ub];
+    s_begin = (int64_t)NHG * off[ub] + (w % NHG) * steps_b;
+    s_end = s_begin + steps_b;
+  } else {
+    const int64_t n_act = active_wgs(total, n_bal);
+    if (w >= n_act) return;
+    s_begin = range_start(w, total, n_act);
+    s_end = range_start(w + 1, total, n_act);
+  }
   if (s_begin >= s_end) return;
 
   // First sequence of the range (binary search over the exclusive offsets).
   int lo = 0, hi = batch - 1;
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
-    if (off[mid] <= s_begin) lo = mid; else hi = mid - 1;
+    if ((int64_t)NHG * off[mid] <= s_begin) lo = mid; else hi = mid - 1;
   }
-  const int first_seq = lo;
 
-  int b = first_seq;
+  int b = lo;
   int64_t s = s_begin;
   while (s < s_end) {
-    while (off[b + 1] <= s) ++b;  // skip empty sequences
-    const int64_t sb = off[b];
-    const int64_t seg_end = min((int64_t)off[b + 1], s_end);
+    while ((int64_t)NHG * off[b + 1] <= s) ++b;  // skip empty sequences
+    const int64_t steps_b = off[b + 1] - off[b];
+    const int64_t sq0 = (int64_t)NHG * off[b];
+    const int hgi = (int)((s - sq0) / steps_b);   // head group of the unit
+    const int64_t sb = sq0 + hgi * steps_b;       // the unit's steps: [sb, sb + steps_b)
+    const int64_t seg_end = min(sb + steps_b, s_end);
+    const int h = hgi * HG + hl;                  // this lane's KV head
+    // Byte offset of this lane's 16 B inside a step: token group tg owns the
+    // kTok consecutive tokens [tg*kTok, +kTok) of the step.
+    const uint32_t lane_off = (uint32_t)(tg * kTok * kRowBytes + (h * kHeadDim + lane16 * 8) * 2);
     int L = seqlens[b] + seqlen_bias;
     L = max(0, min(L, bt_width * kPage));
     const int32_t* bt_row = block_table + (int64_t)b * bt_stride;
@@ -278,18 +332,20 @@ void decode_streamk_split(
 #pragma unroll
     for (int g = 0; g < G; ++g) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) sm_acc[tg][h][g][lane16 * 8 + e] = acc[g][e];
+      for (int e = 0; e < 8; ++e) sm_acc[tg][hl][g][lane16 * 8 + e] = acc[g][e];
       if (lane16 == 0) {
-        sm_ml[tg][h][g][0] = m[g];
-        sm_ml[tg][h][g][1] = l[g];
+        sm_ml[tg][hl][g][0] = m[g];
+        sm_ml[tg][hl][g][1] = l[g];
       }
     }
     __syncthreads();
-    const bool whole = (s == sb) && (seg_end == off[b + 1]);
-    const int slot = (b == first_seq) ? 0 : 1;
-    for (int o = tid; o < HQ * kHeadDim; o += kThreads) {
-      const int qh = o / kHeadDim, d = o % kHeadDim;
-      const int hh = qh / G, g = qh % G;
+    const bool whole = (s == sb) && (seg_end == sb + steps_b);
+    // A workgroup's first and last segments are the only partial ones.
+    const int slot = (s == s_begin) ? 0 : 1;
+    for (int o = tid; o < GQ * kHeadDim; o += kThreads) {
+      const int ql = o / kHeadDim, d = o % kHeadDim;   // query head within the unit
+      const int hh = ql / G, g = ql % G;
+      const int qh = hgi * GQ + ql;
       float M = sm_ml[0][hh][g][0];
 #pragma unroll
       for (int t = 1; t < TG; ++t) M = fmaxf(M, sm_ml[t][hh][g][0]);
@@ -304,7 +360,7 @@ void decode_streamk_split(
         out[(int64_t)b * out_seq_stride + (int64_t)qh * out_head_stride + d] =
             f32_to_bf16(Ls > 0.f ? A / Ls : 0.f);
       } else {
-        float* p = ws + (((int64_t)w * 2 + slot) * HQ + qh) * kSlotStride;
+        float* p = ws + (((int64_t)w * 2 + slot) * HQ + ql) * kSlotStride;
         p[d] = A;
         if (d == 0) {
           p[kHeadDim] = M;
@@ -317,34 +373,51 @@ void decode_streamk_split(
   }
 }
 
-// Combines the partial slots of sequences shared by several workgroups and
-// writes zeros for empty sequences, reading the step offsets the split kernel
-// published after its slots.  One workgroup per (sequence, query head): 16
-// groups of 16 lanes take every 16th sharing workgroup (a lane owns 8 output
-// dims), so up to 16 slots are read at once; the group states are combined
-// through LDS.
-template <int HKV, int G>
+// Unit of (sequence b, query head qh) and its workgroups.  Returns false when
+// the unit needs no merge (empty, written directly in unit mode, or held by one
+// workgroup); otherwise sets its step range [ub, ue), the first and last
+// owning workgroups and the active workgroup count.
+template <int HKV, int G, int HG>
+__device__ __forceinline__ bool unit_owners(const int32_t* __restrict__ ws_off, int batch, int n_bal,
+                                            int b, int qh, int64_t* ub, int64_t* w0, int64_t* w1,
+                                            int64_t* total, int64_t* n_act) {
+  constexpr int NHG = HKV / HG;
+  const int64_t steps_b = ws_off[b + 1] - ws_off[b];
+  if (ws_off[batch + 1] != 0) return false;  // unit mode: every unit was written whole
+  *total = (int64_t)NHG * ws_off[batch];
+  *n_act = active_wgs(*total, n_bal);
+  *ub = (int64_t)NHG * ws_off[b] + (qh / (HG * G)) * steps_b;
+  *w0 = owner_of(*ub, *total, *n_act);
+  *w1 = owner_of(*ub + steps_b - 1, *total, *n_act);
+  return *w0 != *w1;
+}
+
+// Combines the partial slots of units shared by several workgroups and
+// writes zeros for empty sequences, reading the step offsets and the mode the
+// split kernel published after its slots.  One workgroup per (sequence, query
+// head): 16 groups of 16 lanes take every 16th sharing workgroup (a lane owns
+// 8 output dims), so up to 16 slots are read at once; the group states are
+// combined through LDS.
+template <int HKV, int G, int HG>
 __global__ __launch_bounds__(kThreads) void decode_streamk_merge(
-    int batch, int n_wg, const float* __restrict__ ws, uint16_t* __restrict__ out,
+    int batch, int n_bal, const float* __restrict__ ws, uint16_t* __restrict__ out,
     int64_t out_seq_stride, int64_t out_head_stride) {
   constexpr int HQ = HKV * G;
+  constexpr int GQ = HG * G;
   constexpr int kGroups = kThreads / 16;
   __shared__ float s_ml[kGroups][2];
   __shared__ float s_acc[kGroups][kHeadDim];
-  const int32_t* ws_off = reinterpret_cast<const int32_t*>(ws + (int64_t)n_wg * 2 * HQ * kSlotStride);
+  const int32_t* ws_off = reinterpret_cast<const int32_t*>(ws + (int64_t)n_bal * 2 * HQ * kSlotStride);
   const int b = blockIdx.x, qh = blockIdx.y;
   const int tid = threadIdx.x, lane16 = tid & 15, grp = tid >> 4;
   uint16_t* o_row = out + (int64_t)b * out_seq_stride + (int64_t)qh * out_head_stride;
-  const int64_t total = ws_off[batch];
-  const int64_t sb = ws_off[b], se = ws_off[b + 1];
-  if (se == sb) {  // empty sequence attends to nothing: zeros, as flash-attn
+  if (ws_off[b + 1] == ws_off[b]) {  // empty sequence attends to nothing: zeros, as flash-attn
     if (tid < kHeadDim) o_row[tid] = 0;
     return;
   }
-  const int64_t n_act = active_wgs(total, n_wg);
-  const int64_t w0 = owner_of(sb, total, n_act);
-  const int64_t w1 = owner_of(se - 1, total, n_act);
-  if (w0 == w1) return;  // written directly by its only workgroup
+  int64_t ub, w0, w1, total, n_act;
+  if (!unit_owners<HKV, G, HG>(ws_off, batch, n_bal, b, qh, &ub, &w0, &w1, &total, &n_act)) return;
+  const int ql = qh % GQ;
   const int d0 = lane16 * 8;
   float M = kNegBig, Ls = 0.f, A[8];
 #pragma unroll
@@ -352,8 +425,8 @@ __global__ __launch_bounds__(kThreads) void decode_streamk_merge(
   for (int64_t ww = w0 + grp; ww <= w1; ww += kGroups) {
     const int64_t r0 = range_start(ww, total, n_act);
     if (r0 == range_start(ww + 1, total, n_act)) continue;  // empty range: owns no slot
-    const int slot = (r0 >= sb) ? 0 : 1;
-    const float* p = ws + ((ww * 2 + slot) * HQ + qh) * kSlotStride;
+    const int slot = (r0 >= ub) ? 0 : 1;
+    const float* p = ws + ((ww * 2 + slot) * HQ + ql) * kSlotStride;
     const float mw = p[kHeadDim], lw = p[kHeadDim + 1];
     const f32x4_t a0 = *reinterpret_cast<const f32x4_t*>(p + d0);
     const f32x4_t a1 = *reinterpret_cast<const f32x4_t*>(p + d0 + 4);
@@ -389,33 +462,32 @@ __global__ __launch_bounds__(kThreads) void decode_streamk_merge(
   }
 }
 
-// The same combination for large batches (each sequence shared by a few
+// The same combination for large batches (each unit shared by a few
 // workgroups): one workgroup per sequence, a 16-lane group per query head
 // (a lane owns 8 output dims) walking the sharing workgroups, four slots in
 // flight; no LDS.
-template <int HKV, int G>
+template <int HKV, int G, int HG>
 __global__ __launch_bounds__(kThreads) void decode_streamk_merge_seq(
-    int batch, int n_wg, const float* __restrict__ ws, uint16_t* __restrict__ out,
+    int batch, int n_bal, const float* __restrict__ ws, uint16_t* __restrict__ out,
     int64_t out_seq_stride, int64_t out_head_stride) {
   constexpr int HQ = HKV * G;
+  constexpr int GQ = HG * G;
   constexpr int kGroups = kThreads / 16;
-  const int32_t* ws_off = reinterpret_cast<const int32_t*>(ws + (int64_t)n_wg * 2 * HQ * kSlotStride);
+  const int32_t* ws_off = reinterpret_cast<const int32_t*>(ws + (int64_t)n_bal * 2 * HQ * kSlotStride);
   const int b = blockIdx.x;
   const int tid = threadIdx.x, lane16 = tid & 15, grp = tid >> 4;
-  const int64_t total = ws_off[batch];
-  const int64_t sb = ws_off[b], se = ws_off[b + 1];
   uint16_t* o_seq = out + (int64_t)b * out_seq_stride;
   const int d0 = lane16 * 8;
-  if (se == sb) {  // empty sequence attends to nothing: zeros, as flash-attn
+  if (ws_off[b + 1] == ws_off[b]) {  // empty sequence attends to nothing: zeros, as flash-attn
     for (int qh = grp; qh < HQ; qh += kGroups)
       *reinterpret_cast<uint4*>(o_seq + (int64_t)qh * out_head_stride + d0) = make_uint4(0, 0, 0, 0);
     return;
   }
-  const int64_t n_act = active_wgs(total, n_wg);
-  const int64_t w0 = owner_of(sb, total, n_act);
-  const int64_t w1 = owner_of(se - 1, total, n_act);
-  if (w0 == w1) return;  // written directly by its only workgroup
   for (int qh = grp; qh < HQ; qh += kGroups) {
+    int64_t ub, w0, w1, total, n_act;
+    if (!unit_owners<HKV, G, HG>(ws_off, batch, n_bal, b, qh, &ub, &w0, &w1, &total, &n_act))
+      continue;
+    const int ql = qh % GQ;
     float M = kNegBig, Ls = 0.f, A[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) A[e] = 0.f;
@@ -425,13 +497,13 @@ __global__ __launch_bounds__(kThreads) void decode_streamk_merge_seq(
       bool ok[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        // A workgroup with an empty step range owns no slot; w0 owns step sb,
+        // A workgroup with an empty step range owns no slot; w0 owns step ub,
         // so its slot 0 is always written and stands in for such entries.
         const int64_t ww = wb + j;
         const int64_t r0 = range_start(ww, total, n_act);
         ok[j] = ww <= w1 && r0 != range_start(ww + 1, total, n_act);
-        const int64_t slot = ok[j] ? ww * 2 + ((r0 >= sb) ? 0 : 1) : w0 * 2;
-        const float* p = ws + (slot * HQ + qh) * kSlotStride;
+        const int64_t slot = ok[j] ? ww * 2 + ((r0 >= ub) ? 0 : 1) : w0 * 2;
+        const float* p = ws + (slot * HQ + ql) * kSlotStride;
         mw[j] = p[kHeadDim];
         lw[j] = p[kHeadDim + 1];
         a0[j] = *reinterpret_cast<const f32x4_t*>(p + d0);
@@ -479,23 +551,35 @@ static int64_t device_cus() {
   return cache[dev];
 }
 
-// Workgroups of the balanced decode: two per CU, never more than the step
+// KV heads per work unit: all of them below 128 sequences; from 128 sequences
+// the fewest (down to a quarter of the heads, at least 2) that still give two
+// units per workgroup slot of the GPU.
+int64_t streamk_heads_per_unit(int64_t batch, int64_t num_kv_heads) {
+  const int64_t target = 2 * device_cus();
+  int64_t hg = num_kv_heads;
+  if (batch >= 128)
+    while (hg > 2 && hg > num_kv_heads / 4 && batch * (num_kv_heads / hg) < target) hg /= 2;
+  return hg;
+}
+
+// Workgroups of the balanced split: two per CU, never more than the step
 // count can feed.
-int64_t streamk_workgroups(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
-                           int64_t bt_width) {
-  (void)num_q_heads;
-  const int64_t ts = (16 / num_kv_heads) * kTok;
-  const int64_t max_steps = batch * ((bt_width * kPage + ts - 1) / ts);
+static int64_t streamk_balanced_wgs(int64_t batch, int64_t num_kv_heads, int64_t hg,
+                                    int64_t bt_width) {
+  const int64_t ts = (16 / hg) * kTok;
+  const int64_t max_steps = batch * (num_kv_heads / hg) * ((bt_width * kPage + ts - 1) / ts);
   const int64_t target = 2 * device_cus();
   return max_steps < target ? (max_steps < 1 ? 1 : max_steps) : target;
 }
 
 int64_t streamk_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
                                 int64_t bt_width) {
-  // partial slots, then the published step offsets (int32 [batch + 1])
-  return streamk_workgroups(batch, num_q_heads, num_kv_heads, bt_width) * 2 * num_q_heads *
-             kSlotStride * (int64_t)sizeof(float) +
-         (batch + 1) * (int64_t)sizeof(int32_t);
+  // partial slots of the balanced split, then the published step offsets
+  // (int32 [batch + 1]) and the mode word
+  const int64_t hg = streamk_heads_per_unit(batch, num_kv_heads);
+  return streamk_balanced_wgs(batch, num_kv_heads, hg, bt_width) * 2 * num_q_heads * kSlotStride *
+             (int64_t)sizeof(float) +
+         (batch + 2) * (int64_t)sizeof(int32_t);
 }
 
 bool streamk_supported(int64_t num_q_heads, int64_t num_kv_heads, int64_t batch) {
@@ -505,26 +589,28 @@ bool streamk_supported(int64_t num_q_heads, int64_t num_kv_heads, int64_t batch)
   return hkv_ok && (g == 1 || g == 2 || g == 4) && batch <= 65535;
 }
 
-template <int HKV, int G>
+template <int HKV, int G, int HG>
 static int launch(const uint16_t* q, int64_t qs, int64_t qh, const uint16_t* kc, const uint16_t* vc,
                   int64_t nb, const int32_t* lens, int32_t bias, const int32_t* bt, int64_t bts,
                   int64_t btw, int64_t batch, float scale_log2, uint16_t* out, int64_t os,
                   int64_t oh, float* ws, hipStream_t s) {
-  const int64_t n_wg = streamk_workgroups(batch, HKV * G, HKV, btw);
-  hipLaunchKernelGGL((decode_streamk_split<HKV, G>), dim3((unsigned)n_wg), dim3(kThreads), 0, s, q,
-                     qs, qh, kc, vc, nb, lens, (int)bias, bt, bts, (int)btw, (int)batch, (int)n_wg,
-                     scale_log2, out, os, oh, ws);
+  const int64_t n_bal = streamk_balanced_wgs(batch, HKV, HG, btw);
+  const int64_t n_units = batch * (HKV / HG);
+  const int64_t grid = n_bal > n_units ? n_bal : n_units;
+  hipLaunchKernelGGL((decode_streamk_split<HKV, G, HG>), dim3((unsigned)grid), dim3(kThreads), 0, s,
+                     q, qs, qh, kc, vc, nb, lens, (int)bias, bt, bts, (int)btw, (int)batch,
+                     (int)n_bal, scale_log2, out, os, oh, ws);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
-  // Small batches: sequences are shared by many workgroups, so one merge
+  // Small batches: units are shared by many workgroups, so one merge
   // workgroup per (sequence, head) reads 16 slots at once; large batches:
-  // a few slots per sequence, one workgroup per sequence.
+  // a few slots per unit, one workgroup per sequence.
   if (batch >= 128)
-    hipLaunchKernelGGL((decode_streamk_merge_seq<HKV, G>), dim3((unsigned)batch), dim3(kThreads), 0, s,
-                       (int)batch, (int)n_wg, ws, out, os, oh);
+    hipLaunchKernelGGL((decode_streamk_merge_seq<HKV, G, HG>), dim3((unsigned)batch), dim3(kThreads),
+                       0, s, (int)batch, (int)n_bal, ws, out, os, oh);
   else
-    hipLaunchKernelGGL((decode_streamk_merge<HKV, G>), dim3((unsigned)batch, (unsigned)(HKV * G)),
-                       dim3(kThreads), 0, s, (int)batch, (int)n_wg, ws, out, os, oh);
+    hipLaunchKernelGGL((decode_streamk_merge<HKV, G, HG>), dim3((unsigned)batch, (unsigned)(HKV * G)),
+                       dim3(kThreads), 0, s, (int)batch, (int)n_bal, ws, out, os, oh);
   QMI_RETURN_LAUNCH_STATUS();
 }
 
@@ -535,14 +621,17 @@ int launch_streamk(const uint16_t* q, int64_t qs, int64_t qh, const uint16_t* kc
                    hipStream_t s) {
   const float sl = scale * kLog2e;
   const int64_t g = num_q_heads / num_kv_heads;
-#define QMI_SK(HK, GG)                                                                         \
-  if (num_kv_heads == HK && g == GG)                                                           \
-    return launch<HK, GG>(q, qs, qh, kc, vc, nb, lens, bias, bt, bts, btw, batch, sl, out, os, oh, \
-                          ws, s);
-  QMI_SK(8, 2) QMI_SK(8, 1) QMI_SK(8, 4)
-  QMI_SK(4, 1) QMI_SK(4, 2) QMI_SK(4, 4)
-  QMI_SK(2, 1) QMI_SK(2, 2) QMI_SK(2, 4)
-  QMI_SK(16, 1) QMI_SK(16, 2) QMI_SK(16, 4)
+  const int64_t hg = streamk_heads_per_unit(batch, num_kv_heads);
+#define QMI_SK(HK, GG, HGG)                                                                      \
+  if (num_kv_heads == HK && g == GG && hg == HGG)                                                \
+    return launch<HK, GG, HGG>(q, qs, qh, kc, vc, nb, lens, bias, bt, bts, btw, batch, sl, out, os, \
+                               oh, ws, s);
+#define QMI_SK_G(HK, HGG) QMI_SK(HK, 1, HGG) QMI_SK(HK, 2, HGG) QMI_SK(HK, 4, HGG)
+  QMI_SK_G(8, 8) QMI_SK_G(8, 4) QMI_SK_G(8, 2)
+  QMI_SK_G(4, 4) QMI_SK_G(4, 2)
+  QMI_SK_G(2, 2)
+  QMI_SK_G(16, 16) QMI_SK_G(16, 8) QMI_SK_G(16, 4)
+#undef QMI_SK_G
 #undef QMI_SK
   return QMI_E_UNSUPPORTED;
 }

@@ -215,3 +215,88 @@ def test_decode_misaligned_q_view(pkg, gpu):
                                              w["block_tables"].to(gpu), w["scale"])
     torch.cuda.synchronize()
     _check(out, w)
+
+
+def _decode_with_mode(pkg, gpu, w):
+    """Balanced schedule through the C ABI with an explicit workspace; returns
+    (out, unit_mode) where unit_mode is the mode word the split kernel
+    publishes as the last int32 of its workspace."""
+    L = pkg._lib.lib()
+    q = w["q"].to(gpu)
+    kc, vc = w["k_cache"].to(gpu), w["v_cache"].to(gpu)
+    lens = w["cache_seqlens"].to(gpu)
+    bt = w["block_tables"].to(gpu)
+    bsz, hq, d = q.shape
+    nb, _, hkv, _ = kc.shape
+    out = torch.empty_like(q)
+    nbytes = L.qmi_paged_decode_workspace_bytes(bsz, hkv, hq, bt.shape[1], 0)
+    ws = torch.zeros(nbytes // 4, dtype=torch.int32, device=gpu)
+    st = L.qmi_paged_decode_attention(
+        q.data_ptr(), q.stride(0), q.stride(1), kc.data_ptr(), vc.data_ptr(), nb, 256, hq, hkv,
+        d, lens.data_ptr(), 0, bt.data_ptr(), bt.stride(0), bt.shape[1], bsz, w["scale"],
+        out.data_ptr(), out.stride(0), out.stride(1), ws.data_ptr(), nbytes, 0,
+        torch.cuda.current_stream(gpu).cuda_stream)
+    pkg._lib.check(st, "paged_decode_attention")
+    torch.cuda.synchronize()
+    return out, int(ws[-1].item())
+
+
+@pytest.mark.parametrize("bsz,hq,hkv", [(256, 16, 8), (128, 16, 8), (256, 16, 4), (300, 32, 16)])
+def test_decode_unit_mode_near_equal_lengths(pkg, gpu, bsz, hq, hkv):
+    """Batches of 128+ sequences of nearly equal length (a GRPO rollout) run
+    one whole (sequence, head group) unit per workgroup with nothing to merge;
+    a few empty sequences do not change that."""
+    g = torch.Generator().manual_seed(80 + bsz + hkv)
+    lens = torch.randint(600, 641, (bsz,), generator=g).tolist()
+    lens[3] = lens[bsz - 1] = 0
+    w = _ragged(81 + bsz, lens, hq=hq, hkv=hkv)
+    print(f"[decode] unit mode B={bsz} {hq}/{hkv}", flush=True)
+    out, mode = _decode_with_mode(pkg, gpu, w)
+    assert mode == 1
+    assert out[[3, bsz - 1]].abs().max().item() == 0.0
+    _check(out, w)
+
+
+@pytest.mark.parametrize("bsz", [128, 256])
+def test_decode_head_group_units_ragged(pkg, gpu, bsz):
+    """Ragged lengths at 128+ sequences: the balanced split runs over
+    (sequence, head group) units, which then straddle workgroups and merge."""
+    g = torch.Generator().manual_seed(90 + bsz)
+    lens = torch.randint(1, 1500, (bsz,), generator=g).tolist()
+    lens[0] = 0
+    w = _ragged(91 + bsz, lens)
+    print(f"[decode] head-group units ragged B={bsz}", flush=True)
+    out, mode = _decode_with_mode(pkg, gpu, w)
+    assert mode == 0
+    _check(out, w)
+
+
+def test_decode_graph_replay_switches_unit_mode(pkg, gpu):
+    """One captured graph, replayed with lengths that select unit mode and
+    then the balanced split (and back): every replay equals the eager call."""
+    bsz = 256
+    g = torch.Generator().manual_seed(95)
+    w = _ragged(96, [900] * bsz)
+    q = w["q"].to(gpu)
+    kc, vc = w["k_cache"].to(gpu), w["v_cache"].to(gpu)
+    lens = w["cache_seqlens"].to(gpu)
+    bt = w["block_tables"].to(gpu)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        pkg.kernels.paged_decode_attention(q, kc, vc, lens, bt, w["scale"])
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = pkg.kernels.paged_decode_attention(q, kc, vc, lens, bt, w["scale"])
+    print("[decode] graph replay across unit mode", flush=True)
+    for it, (lo, hi) in enumerate([(880, 900), (1, 900), (700, 720), (0, 400)]):
+        new = torch.randint(lo, hi + 1, (bsz,), generator=g, dtype=torch.int32)
+        lens.copy_(new)
+        q.copy_(torch.randn(q.shape, generator=g).to(torch.bfloat16))
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = pkg.kernels.paged_decode_attention(q, kc, vc, lens, bt, w["scale"])
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {it}"
+        _check(out, dict(w, q=q.cpu(), cache_seqlens=lens.cpu()))
