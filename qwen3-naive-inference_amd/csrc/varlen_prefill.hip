@@ -16,14 +16,18 @@
 //     feeds two MFMAs and the K/V tiles staged in LDS serve all G heads.
 //   * Scores are computed transposed, S^T = K Q^T, with
 //     v_mfma_f32_16x16x32_bf16 (A = 16 keys x 32 dims from LDS, B = Q^T held
-//     in registers).  Its accumulator layout (lane l: keys 4*(l/16)+r,
+//     in registers).  The K operands of a 32-dim slice are read from LDS two
+//     slices ahead of their MFMAs (inline-asm ds_read_b128 with explicit
+//     LDS-counter waits; left to itself the compiler sinks each read next to
+//     the MFMA that consumes it and the LDS latency shows on every slice).  Its accumulator layout (lane l: keys 4*(l/16)+r,
 //     query l%16) is exactly the B-operand layout of the second product
 //     O^T = V^T P^T once two 16-key blocks are packed to bf16, so P never
 //     leaves registers.
 //   * K and V tiles are staged through registers: each lane loads its
-//     16-byte chunks of the next tile from the page (8 per tile) while the
-//     current tile is computed, then writes them to LDS (ds_write_b128, a
-//     wave-wide write fills 1 KB, lane l at base + 16 l).
+//     16-byte chunks of the next tile from the page (8 per tile) once the
+//     current tile's QK product is done (so the staging registers are not
+//     live beside the K operands), then writes them to LDS at the end of the
+//     tile (ds_write_b128, a wave-wide write fills 1 KB, lane l at base + 16 l).
 //     Rows are 256 bytes (one KV head of a token) with the 16-byte chunks
 //     XOR-swizzled instead of padded: chunk c of K row r sits at c ^ (r % 16)
 //     (16 consecutive rows then hit 16 distinct 4-bank groups for the A
@@ -95,6 +99,22 @@ __device__ __forceinline__ v2u_t ds_read_tr16_b64(uint32_t addr) {
 // tied to the wait so that no use of them is scheduled above it.
 template <int N>
 __device__ __forceinline__ void lgkm_wait(v2u_t& a, v2u_t& b, v2u_t& c, v2u_t& d) {
+  asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "i"(N) : "memory");
+}
+
+// LDS read of 16 bytes (ds_read_b128) at a per-lane address plus an
+// immediate byte offset; as inline asm it stays where it is written instead
+// of being sunk next to its use.  The caller waits with lgkm_wait_u4.
+typedef __attribute__((ext_vector_type(4))) unsigned int u4v_t;
+template <int OFF>
+__device__ __forceinline__ u4v_t ds_read_b128_at(uint32_t addr) {
+  u4v_t r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF) : "memory");
+  return r;
+}
+
+template <int N>
+__device__ __forceinline__ void lgkm_wait_u4(u4v_t& a, u4v_t& b, u4v_t& c, u4v_t& d) {
   asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "i"(N) : "memory");
 }
 
@@ -271,9 +291,12 @@ void varlen_prefill_kernel(
   // loop is unrolled by buffer), so no address arithmetic is left per tile.
   // K operand of key block kb, dim slice c: row 16 kb + l16, logical chunk
   // 4c + g4, stored at physical chunk (4c + g4) ^ l16.
-  uint32_t k_lane[4];
+  uint32_t k_rd[4];  // LDS byte address of the lane's K chunk of slice c, buffer 0, key block 0
+  {
+    const uint32_t sk0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)&sK[0][0];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) k_lane[c] = (uint32_t)(l16 * kHeadDim * 2 + 16 * ((4 * c + g4) ^ l16));
+    for (int c = 0; c < 4; ++c) k_rd[c] = sk0 + (uint32_t)(l16 * kHeadDim * 2 + 16 * ((4 * c + g4) ^ l16));
+  }
   // V^T transpose reads of dim block db, key half c: lane i points at row
   // R = 32c + 4 g4 + l16 / 4 (+16 for the second read), logical 8-byte piece
   // 4 db + l16 % 4, i.e. chunk 2 db + x with x = (l16 % 4) / 2, stored at
@@ -289,7 +312,6 @@ void varlen_prefill_kernel(
     for (int d = 0; d < 8; ++d)
       v_lane[d] = sv0 + (uint32_t)(vrow * kHeadDim * 2 + 8 * (l16 & 1) + 16 * vx + 32 * (d ^ w));
   }
-  const char* sk_bytes = reinterpret_cast<const char*>(&sK[0][0]);
 
   float m_run[2] = {kNegBig, kNegBig};  // running max (log2 domain) per query
   f32x4_t acc_l[2];                     // row 0 (lanes 0-15): running sum of P (bf16) per query
@@ -302,44 +324,50 @@ void varlen_prefill_kernel(
 
   // One tile: tile t sits in LDS buffer BUF (a compile-time constant).  The
   // next tile's loads are issued on every step (the last tile of a segment
-  // reloads itself into the idle buffer), so every path through the loop
-  // leaves the same loads outstanding and the compiler's waits stay at the
-  // LDS writes instead of moving to the top of the tile.
+  // reloads itself into the idle buffer), after the QK product when the tile
+  // is computed, so every path through the loop leaves the same loads
+  // outstanding and the compiler's waits stay at the LDS writes.
   auto tile_step = [&](int t, int t_last, auto buf_c) __attribute__((always_inline)) {
     constexpr int buf = decltype(buf_c)::value;
     const bool compute = tile_ok[buf];  // wave-uniform
-    load_tile(min(t + 1, t_last), buf ^ 1);
     if (compute) {
 
     // ---- S^T = K Q^T for 4 blocks of 16 keys x 2 blocks of 16 queries ----
-    // The K operands of dim slice c+1 are read from LDS while the MFMAs of
-    // slice c run.
+    // The K operands of dim slice c (4 key blocks, 16 rows = 4 KB apart) are
+    // read two slices ahead of their MFMAs, three buffers in rotation.
     f32x4_t s[2][4];
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) s[j][kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    auto kchunk = [&](int kb, int c) {
-      return as_bf16x8(*reinterpret_cast<const uint4*>(sk_bytes + buf * kKeyTile * kHeadDim * 2 +
-                                                        kb * 16 * kHeadDim * 2 + k_lane[c]));
-    };
-    bf16x8_t kop[2][4];
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) kop[0][kb] = kchunk(kb, 0);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      if (c + 1 < 4) {
+    {
+      constexpr int kAhead = 2;
+      u4v_t kop[kAhead + 1][4];
+      auto kissue = [&](auto c_c) __attribute__((always_inline)) {
+        constexpr int c = decltype(c_c)::value;
+        constexpr int off = buf * kKeyTile * kHeadDim * 2;
+        const uint32_t ad = k_rd[c];
+        kop[c % (kAhead + 1)][0] = ds_read_b128_at<off>(ad);
+        kop[c % (kAhead + 1)][1] = ds_read_b128_at<off + 4096>(ad);
+        kop[c % (kAhead + 1)][2] = ds_read_b128_at<off + 8192>(ad);
+        kop[c % (kAhead + 1)][3] = ds_read_b128_at<off + 12288>(ad);
+      };
+      static_for<0, kAhead>([&](auto c_c) __attribute__((always_inline)) { kissue(c_c); });
+      static_for<0, 4>([&](auto c_c) __attribute__((always_inline)) {
+        constexpr int c = decltype(c_c)::value, nxt = c + kAhead, st = c % (kAhead + 1);
+        if constexpr (nxt < 4) kissue(std::integral_constant<int, nxt>{});
+        // LDS reads still outstanding once slice c has arrived: the slices after it.
+        constexpr int later = nxt < 4 ? kAhead : 3 - c;
+        lgkm_wait_u4<4 * later>(kop[st][0], kop[st][1], kop[st][2], kop[st][3]);
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb)
-          kop[(c + 1) & 1][kb] = kchunk(kb, c + 1);
-      }
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          s[j][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[c & 1][kb], qop[j][c], s[j][kb],
-                                                             0, 0, 0);
+          for (int j = 0; j < 2; ++j)
+            s[j][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kop[st][kb]),
+                                                               qop[j][c], s[j][kb], 0, 0, 0);
+      });
     }
+    load_tile(min(t + 1, t_last), buf ^ 1);
 
     // ---- per query block: mask, online softmax, P^T packed to bf16 ----
     // Scores stay unscaled; p = exp2(s * scale_log2 - m).  The running max m
@@ -442,7 +470,9 @@ void varlen_prefill_kernel(
           for (int j = 0; j < 2; ++j)
             acc_l[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pop[j][c], acc_l[j], 0, 0, 0);
       }
-    }  // compute
+    } else {  // compute
+      load_tile(min(t + 1, t_last), buf ^ 1);
+    }
     store_tile(buf ^ 1);
     __syncthreads();
   };
