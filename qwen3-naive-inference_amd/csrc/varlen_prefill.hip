@@ -182,7 +182,7 @@ void varlen_prefill_kernel(
   const int qblk = n_qblocks - 1 - (int)(blockIdx.z % n_qblocks);  // late (long) blocks first
   const int part = (int)(blockIdx.z / n_qblocks);
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: an SGPR
   const int lane = tid & 63;
   const int l16 = lane & 15;
   const int g4 = lane >> 4;

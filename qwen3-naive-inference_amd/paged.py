@@ -212,6 +212,24 @@ def prepare_step(seqs: list[Sequence], device=None, block_size: int = BLOCK_SIZE
             _to_device(build_block_tables(seqs), device))
 
 
+def fill_decode_inputs(seqs: list[Sequence], ids: np.ndarray, pos: np.ndarray, ctx: np.ndarray,
+                       slot: np.ndarray, tables: np.ndarray, block_size: int = BLOCK_SIZE) -> None:
+    """The decode inputs of ``prepare_decode`` written into rows ``0 .. len(seqs)-1``
+    of caller-provided host arrays (``tables`` is ``[rows, W]``, -1 past each
+    table); rows past ``len(seqs)`` are left to the caller."""
+    n = len(seqs)
+    ids[:n] = np.fromiter((s.last_token for s in seqs), dtype=np.int64, count=n)
+    pos[:n] = np.fromiter((s.num_tokens - 1 for s in seqs), dtype=np.int64, count=n)
+    ctx[:n] = np.fromiter((s.kv_len for s in seqs), dtype=np.int32, count=n)
+    slot[:n] = np.fromiter((s.block_table[s.kv_len // block_size] * block_size + s.kv_len % block_size
+                            for s in seqs), dtype=np.int32, count=n)
+    tables[:n] = -1
+    w = tables.shape[1]
+    for i, sq in enumerate(seqs):
+        m = min(len(sq.block_table), w)
+        tables[i, :m] = sq.block_table[:m]
+
+
 def prepare_decode(seqs: list[Sequence], device=None, block_size: int = BLOCK_SIZE,
                    width: int | None = None):
     """Decode inputs (qwen3_naive.py:1207-1225): last token, its position

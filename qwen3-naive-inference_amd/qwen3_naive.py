@@ -31,7 +31,8 @@ import torch.nn.functional as F
 
 from . import kernels as K
 from .kernels import store_kvcache  # noqa: F401  (reference import surface)
-from .paged import BLOCK_SIZE, BlockManager, Sequence, build_block_tables, prepare_decode, prepare_step
+from .paged import (BLOCK_SIZE, BlockManager, Sequence, build_block_tables, fill_decode_inputs,
+                    prepare_decode, prepare_step)
 
 
 @dataclass
@@ -407,15 +408,23 @@ class Qwen3ForCausalLM(nn.Module):
         dev = next(self.parameters()).device
         full = min(self._num_blocks, -(-self.config.max_position_embeddings // self.BLOCK_SIZE))
         bt_width = full if bt_width is None else min(bt_width, full)
+        # Every decode input in one int32 device buffer, field after field
+        # (ids and positions as int64 pairs, then slots, context lengths and
+        # the page tables), so a step's inputs arrive in one host-to-device copy.
+        self._graph_in = torch.zeros(6 * max_bs + max_bs * bt_width, dtype=torch.int32, device=dev)
+        self._graph_max_bs = max_bs
+        v = self._graph_in
         self._graph_bufs = {
-            "input_ids": torch.zeros(max_bs, dtype=torch.long, device=dev),
-            "positions": torch.zeros(max_bs, dtype=torch.long, device=dev),
-            "slot_mapping": torch.full((max_bs,), -1, dtype=torch.int32, device=dev),
-            "context_lens": torch.zeros(max_bs, dtype=torch.int32, device=dev),
-            "block_tables": torch.full((max_bs, bt_width), -1, dtype=torch.int32, device=dev),
+            "input_ids": v[0:2 * max_bs].view(torch.long),
+            "positions": v[2 * max_bs:4 * max_bs].view(torch.long),
+            "slot_mapping": v[4 * max_bs:5 * max_bs],
+            "context_lens": v[5 * max_bs:6 * max_bs],
+            "block_tables": v[6 * max_bs:].view(max_bs, bt_width),
             "outputs": torch.zeros(max_bs, self.config.hidden_size, dtype=torch.bfloat16,
                                    device=dev),
         }
+        self._graph_bufs["slot_mapping"].fill_(-1)
+        self._graph_bufs["block_tables"].fill_(-1)
         self._graphs = {}
         self._graph_pool = None
         self._has_cuda_graphs = False
@@ -463,6 +472,36 @@ class Qwen3ForCausalLM(nn.Module):
         bufs["context_lens"][bs:graph_bs] = 0
         bufs["block_tables"][:bs, :block_tables.shape[1]] = block_tables
         bufs["block_tables"][:bs, block_tables.shape[1]:] = -1
+        self._graphs[graph_bs].replay()
+        return bufs["outputs"][:bs]
+
+    def _run_decode_graph_seqs(self, seqs, ids_dev=None):
+        """Graph decode step straight from the sequences: the inputs of the
+        bucket's rows (padding rows: slot -1, empty context, -1 tables) are
+        written into a pinned host image of the input buffer and sent in one
+        copy; ``ids_dev`` (device token ids, e.g. the previous step's samples)
+        replaces the host ids.  Returns None when no captured graph fits."""
+        bs = len(seqs)
+        graph_bs = next((b for b in sorted(self._graphs) if b >= bs), None)
+        bufs = self._graph_bufs
+        width = bufs["block_tables"].shape[1]
+        if graph_bs is None or max(len(s.block_table) for s in seqs) > width:
+            return None
+        mb = self._graph_max_bs
+        host = torch.empty(self._graph_in.numel(), dtype=torch.int32, pin_memory=True)
+        a = host.numpy()
+        ids, pos = a[0:2 * mb].view(np.int64), a[2 * mb:4 * mb].view(np.int64)
+        slot, ctx = a[4 * mb:5 * mb], a[5 * mb:6 * mb]
+        tables = a[6 * mb:].reshape(mb, width)
+        fill_decode_inputs(seqs, ids, pos, ctx, slot, tables, self.BLOCK_SIZE)
+        ids[bs:graph_bs] = 0
+        pos[bs:graph_bs] = 0
+        slot[bs:graph_bs] = -1
+        ctx[bs:graph_bs] = 0
+        tables[bs:graph_bs] = -1
+        self._graph_in.copy_(host, non_blocking=True)
+        if ids_dev is not None:
+            bufs["input_ids"][:bs].copy_(ids_dev)
         self._graphs[graph_bs].replay()
         return bufs["outputs"][:bs]
 
@@ -631,16 +670,17 @@ class Qwen3ForCausalLM(nn.Module):
                     else:
                         ids_dev = pending["tok_dev"][torch.tensor(idx, device=dev)]
                 self.last_stats["decode_steps"] += 1
-                ids, pos, ctx, bt, slots = self._prepare_decode(scheduled)
                 if ids_dev is not None:
-                    ids = ids_dev
                     self.last_stats["lookahead_steps"] += 1
                 h = None
                 if use_graphs and self._has_cuda_graphs:
-                    h = self._run_decode_graph(len(scheduled), ids, pos, ctx, bt, slots)
+                    h = self._run_decode_graph_seqs(scheduled, ids_dev)
                     if h is not None:
                         self.last_stats["graph_steps"] += 1
                 if h is None:
+                    ids, pos, ctx, bt, slots = self._prepare_decode(scheduled)
+                    if ids_dev is not None:
+                        ids = ids_dev
                     h = self.model.forward_decode(ids, pos, ctx, bt, slots)
                 nxt, lp = self._sample(self.lm_head(h), temperature, top_k, with_logprobs)
                 n = len(scheduled)
@@ -671,13 +711,13 @@ class Qwen3ForCausalLM(nn.Module):
             flush()
             if all_decode:
                 self.last_stats["decode_steps"] += 1
-                ids, pos, ctx, bt, slots = self._prepare_decode(scheduled)
                 h = None
                 if use_graphs and self._has_cuda_graphs:
-                    h = self._run_decode_graph(len(scheduled), ids, pos, ctx, bt, slots)
+                    h = self._run_decode_graph_seqs(scheduled)
                     if h is not None:
                         self.last_stats["graph_steps"] += 1
                 if h is None:
+                    ids, pos, ctx, bt, slots = self._prepare_decode(scheduled)
                     h = self.model.forward_decode(ids, pos, ctx, bt, slots)
                 sample_idx = None
             else:

@@ -193,6 +193,32 @@ def test_prepare_decode_slots():
     assert ctx.tolist() == [255] and pos.tolist() == [255] and ids.tolist() == [3]
 
 
+def test_fill_decode_inputs_matches_prepare_decode():
+    """The graph path writes the decode inputs into preallocated host rows;
+    they equal prepare_decode's, rows past the batch stay untouched and the
+    tables are -1 beyond each sequence's pages."""
+    bm = BM(64)
+    seqs = []
+    for n in (1, 255, 256, 600, 40):
+        sq = Seq(list(range(n)))
+        bm.allocate(sq)
+        sq.kv_len = n
+        sq.append_token(7 + n)
+        bm.may_append(sq)
+        seqs.append(sq)
+    ids, pos, ctx, bt, slot = paged.prepare_decode(seqs, width=6)
+    rows = 8
+    h_ids, h_pos = np.full(rows, 99, np.int64), np.full(rows, 99, np.int64)
+    h_ctx, h_slot = np.full(rows, 99, np.int32), np.full(rows, 99, np.int32)
+    h_bt = np.full((rows, 6), 99, np.int32)
+    paged.fill_decode_inputs(seqs, h_ids, h_pos, h_ctx, h_slot, h_bt)
+    n = len(seqs)
+    assert h_ids[:n].tolist() == ids.tolist() and h_pos[:n].tolist() == pos.tolist()
+    assert h_ctx[:n].tolist() == ctx.tolist() and h_slot[:n].tolist() == slot.tolist()
+    assert h_bt[:n].tolist() == bt.tolist()
+    assert (h_ids[n:] == 99).all() and (h_bt[n:] == 99).all()
+
+
 def test_scheduler_lifo_preemption():
     """At a page boundary with no free page, the newest running sequence is
     preempted: its pages are freed, it restarts from its prompt and goes to
