@@ -80,8 +80,13 @@ int qmi_store_kvcache(const uint16_t* key, int64_t key_row_stride,
  * heads; num_kv_heads in {2, 4, 8, 16}, ratio in {1, 2, 4}, batch <= 1024,
  * out 16-byte aligned with strides a multiple of 8) when it applies, else an
  * automatic per-(sequence, KV head) split; pages_per_split > 0 forces the
- * per-(sequence, KV head) split with that many pages.  With
- * pages_per_split <= 0 the workspace size covers either schedule.
+ * per-(sequence, KV head) split with that many pages.  pages_per_split == -1
+ * selects the balanced schedule's whole-unit form: each workgroup takes one
+ * whole (sequence, KV-head group) unit, empty sequences are written as zeros
+ * and no merge launch follows; it is correct for any lengths and pays off
+ * when the context lengths are near-equal (the caller's choice: the default
+ * form detects that case on the device too, but still launches its merge).
+ * With pages_per_split <= 0 the workspace size covers either schedule.
  * Pages whose table entry is outside [0, num_blocks) contribute nothing;
  * num_blocks == 0 is rejected (QMI_E_BAD_SHAPE).
  */

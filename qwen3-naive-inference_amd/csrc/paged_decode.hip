@@ -320,7 +320,7 @@ int launch_streamk(const uint16_t* q, int64_t qs, int64_t qh, const uint16_t* kc
                    const uint16_t* vc, int64_t nb, int64_t num_q_heads, int64_t num_kv_heads,
                    const int32_t* lens, int32_t bias, const int32_t* bt, int64_t bts, int64_t btw,
                    int64_t batch, float scale, uint16_t* out, int64_t os, int64_t oh, float* ws,
-                   hipStream_t s);
+                   bool whole_units, hipStream_t s);
 }  // namespace qmi
 
 extern "C" int64_t qmi_paged_decode_workspace_bytes(int64_t batch, int64_t num_kv_heads,
@@ -373,7 +373,7 @@ extern "C" int qmi_paged_decode_attention(
     return qmi::launch_streamk(q, q_seq_stride, q_head_stride, k_cache, v_cache, num_blocks,
                                num_q_heads, num_kv_heads, seqlens, seqlen_bias, block_table,
                                bt_stride, bt_width, batch, scale, out, out_seq_stride,
-                               out_head_stride, workspace, s);
+                               out_head_stride, workspace, pages_per_split == -1, s);
   }
   const int64_t pps = pages_per_split > 0 ? pages_per_split
                                           : auto_pages_per_split(batch, num_kv_heads, bt_width);

@@ -152,7 +152,7 @@ void decode_streamk_split(
     int64_t num_blocks, const int32_t* __restrict__ seqlens, int seqlen_bias,
     const int32_t* __restrict__ block_table, int64_t bt_stride, int bt_width, int batch,
     int n_bal, float scale_log2, uint16_t* __restrict__ out, int64_t out_seq_stride,
-    int64_t out_head_stride, float* __restrict__ ws) {
+    int64_t out_head_stride, float* __restrict__ ws, int force_units) {
   constexpr int NHG = HKV / HG;                          // units (head groups) per sequence
   constexpr int TG = kTokGroups<HG>;
   constexpr int TS = kStepTokens<HG>;
@@ -174,21 +174,33 @@ void decode_streamk_split(
   scan_steps<kThreads, TS>(seqlens, seqlen_bias, bt_width, batch, off, &sm_max_steps);
   const int64_t total = (int64_t)NHG * off[batch];      // unit steps of the launch
   const int64_t n_units = (int64_t)batch * NHG;
-  const bool unit_mode = use_unit_mode(total, sm_max_steps, n_units, gridDim.x, n_bal);
+  // Whole units are forced by the caller (no merge launch follows) or chosen
+  // here when the lengths are near-equal.
+  const bool unit_mode =
+      force_units != 0 || use_unit_mode(total, sm_max_steps, n_units, gridDim.x, n_bal);
   if (w == 0) {  // publish the step offsets and the mode for the merge kernel
     int32_t* ws_off = reinterpret_cast<int32_t*>(ws + (int64_t)n_bal * 2 * HQ * kSlotStride);
     for (int i = tid; i <= batch; i += kThreads) ws_off[i] = off[i];
     if (tid == 0) ws_off[batch + 1] = unit_mode ? 1 : 0;
   }
-  if (total == 0) return;
   int64_t s_begin, s_end;
-  if (unit_mode) {  // one whole unit per workgroup
+  if (unit_mode) {  // one whole unit per workgroup (grid >= units)
     if (w >= n_units) return;
     const int ub = (int)(w / NHG);
     const int64_t steps_b = off[ub + 1] - off[ub];
+    if (steps_b == 0) {  // empty sequence attends to nothing: zeros, as flash-attn
+      uint16_t* o_seq = out + (int64_t)ub * out_seq_stride;
+      for (int i = tid; i < GQ * (kHeadDim / 8); i += kThreads) {
+        const int qh = (int)(w % NHG) * GQ + i / (kHeadDim / 8);
+        *reinterpret_cast<uint4*>(o_seq + (int64_t)qh * out_head_stride + (i % (kHeadDim / 8)) * 8) =
+            make_uint4(0u, 0u, 0u, 0u);
+      }
+      return;
+    }
     s_begin = (int64_t)NHG * off[ub] + (w % NHG) * steps_b;
     s_end = s_begin + steps_b;
   } else {
+    if (total == 0) return;
     const int64_t n_act = active_wgs(total, n_bal);
     if (w >= n_act) return;
     s_begin = range_start(w, total, n_act);
@@ -593,15 +605,16 @@ template <int HKV, int G, int HG>
 static int launch(const uint16_t* q, int64_t qs, int64_t qh, const uint16_t* kc, const uint16_t* vc,
                   int64_t nb, const int32_t* lens, int32_t bias, const int32_t* bt, int64_t bts,
                   int64_t btw, int64_t batch, float scale_log2, uint16_t* out, int64_t os,
-                  int64_t oh, float* ws, hipStream_t s) {
+                  int64_t oh, float* ws, bool whole_units, hipStream_t s) {
   const int64_t n_bal = streamk_balanced_wgs(batch, HKV, HG, btw);
   const int64_t n_units = batch * (HKV / HG);
   const int64_t grid = n_bal > n_units ? n_bal : n_units;
   hipLaunchKernelGGL((decode_streamk_split<HKV, G, HG>), dim3((unsigned)grid), dim3(kThreads), 0, s,
                      q, qs, qh, kc, vc, nb, lens, (int)bias, bt, bts, (int)btw, (int)batch,
-                     (int)n_bal, scale_log2, out, os, oh, ws);
+                     (int)n_bal, scale_log2, out, os, oh, ws, whole_units ? 1 : 0);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
+  if (whole_units) return QMI_OK;  // every unit was written whole, empty ones as zeros
   // Small batches: units are shared by many workgroups, so one merge
   // workgroup per (sequence, head) reads 16 slots at once; large batches:
   // a few slots per unit, one workgroup per sequence.
@@ -618,14 +631,14 @@ int launch_streamk(const uint16_t* q, int64_t qs, int64_t qh, const uint16_t* kc
                    const uint16_t* vc, int64_t nb, int64_t num_q_heads, int64_t num_kv_heads,
                    const int32_t* lens, int32_t bias, const int32_t* bt, int64_t bts, int64_t btw,
                    int64_t batch, float scale, uint16_t* out, int64_t os, int64_t oh, float* ws,
-                   hipStream_t s) {
+                   bool whole_units, hipStream_t s) {
   const float sl = scale * kLog2e;
   const int64_t g = num_q_heads / num_kv_heads;
   const int64_t hg = streamk_heads_per_unit(batch, num_kv_heads);
 #define QMI_SK(HK, GG, HGG)                                                                      \
   if (num_kv_heads == HK && g == GG && hg == HGG)                                                \
     return launch<HK, GG, HGG>(q, qs, qh, kc, vc, nb, lens, bias, bt, bts, btw, batch, sl, out, os, \
-                               oh, ws, s);
+                               oh, ws, whole_units, s);
 #define QMI_SK_G(HK, HGG) QMI_SK(HK, 1, HGG) QMI_SK(HK, 2, HGG) QMI_SK(HK, 4, HGG)
   QMI_SK_G(8, 8) QMI_SK_G(8, 4) QMI_SK_G(8, 2)
   QMI_SK_G(4, 4) QMI_SK_G(4, 2)

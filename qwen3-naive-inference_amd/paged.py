@@ -230,6 +230,18 @@ def fill_decode_inputs(seqs: list[Sequence], ids: np.ndarray, pos: np.ndarray, c
         tables[i, :m] = sq.block_table[:m]
 
 
+def near_equal_contexts(ctx: np.ndarray) -> bool:
+    """True when every row's key count (context + 1) is within 10% of the
+    rows' mean: the decode attention then runs one whole (sequence, head
+    group) unit per workgroup with no merge, since the longest unit is not
+    much longer than a balanced share.  ``ctx`` holds the context lengths of
+    every row the kernel sees (padding rows included)."""
+    if len(ctx) == 0:
+        return False
+    keys = ctx.astype(np.int64) + 1
+    return 10 * int(keys.max()) * len(keys) <= 11 * int(keys.sum())
+
+
 def prepare_decode(seqs: list[Sequence], device=None, block_size: int = BLOCK_SIZE,
                    width: int | None = None):
     """Decode inputs (qwen3_naive.py:1207-1225): last token, its position

@@ -32,7 +32,7 @@ import torch.nn.functional as F
 from . import kernels as K
 from .kernels import store_kvcache  # noqa: F401  (reference import surface)
 from .paged import (BLOCK_SIZE, BlockManager, Sequence, build_block_tables, fill_decode_inputs,
-                    prepare_decode, prepare_step)
+                    near_equal_contexts, prepare_decode, prepare_step)
 
 
 @dataclass
@@ -157,6 +157,10 @@ class Qwen3Attention(nn.Module):
         self.k_norm = RMSNorm(self.head_dim, eps=config.rms_norm_eps)
         self.k_cache = None
         self.v_cache = None
+        # Decode schedule passed to the attention kernel: 0 = balanced split
+        # with merge, -1 = one whole (sequence, head group) unit per
+        # workgroup and no merge (the engine picks it for near-equal contexts).
+        self.decode_pages_per_split = 0
         # Not a registered submodule: the cache is shared between layers.
         self.__dict__["rotary_emb"] = get_rope(self.head_dim, config.max_position_embeddings,
                                                config.rope_theta)
@@ -231,7 +235,8 @@ class Qwen3Attention(nn.Module):
             slot_mapping = (blk * BLOCK_SIZE + ctx % BLOCK_SIZE).to(torch.int32)
         q = self._project_store(x, positions, slot_mapping)
         o = K.paged_decode_attention(q, self.k_cache, self.v_cache, context_lens, block_tables,
-                                     self.scale, seqlen_bias=1)
+                                     self.scale, seqlen_bias=1,
+                                     pages_per_split=self.decode_pages_per_split)
         return self.o_proj(o.view(batch, -1))
 
 
@@ -323,6 +328,9 @@ class Qwen3Model(nn.Module):
 # Decode batch sizes captured as HIP graphs.  The reference stops at 64 and
 # runs larger batches eagerly; the 288 GB HBM affords buckets up to 256.
 GRAPH_BATCH_SIZES = (1, 2, 4, 8, 16, 32, 48, 64, 96, 128, 160, 192, 256)
+# Buckets that also get a whole-unit decode graph: from 128 sequences the
+# attention's (sequence, head group) units fill two workgroups per CU.
+UNIT_GRAPH_MIN_BS = 128
 MAX_TOKENS_PER_STEP = 2048
 # Stands in for a sampled token whose value is still on the device (decode lookahead).
 _PENDING_TOKEN = -1
@@ -346,6 +354,7 @@ class Qwen3ForCausalLM(nn.Module):
             self.lm_head.weight = self.model.embed_tokens.weight
         self._num_blocks = 0
         self._graphs: dict = {}
+        self._graphs_units: dict = {}
         self._graph_bufs = None
         self._graph_pool = None
         self._has_cuda_graphs = False
@@ -395,6 +404,7 @@ class Qwen3ForCausalLM(nn.Module):
         for layer in self.model.layers:
             layer.self_attn.k_cache = layer.self_attn.v_cache = None
         self._graphs.clear()
+        self._graphs_units.clear()
         self._has_cuda_graphs = False
         torch.cuda.empty_cache()
         k = torch.empty((n,) + shape, dtype=torch.bfloat16, device=dev)
@@ -426,18 +436,29 @@ class Qwen3ForCausalLM(nn.Module):
         self._graph_bufs["slot_mapping"].fill_(-1)
         self._graph_bufs["block_tables"].fill_(-1)
         self._graphs = {}
+        self._graphs_units = {}
         self._graph_pool = None
         self._has_cuda_graphs = False
+
+    def _set_decode_schedule(self, pages_per_split: int) -> None:
+        for layer in self.model.layers:
+            layer.self_attn.decode_pages_per_split = pages_per_split
 
     def _capture_decode_graphs(self, batch_sizes=GRAPH_BATCH_SIZES):
         """Capture forward_decode for each bucket into one shared memory pool.
         Padded rows carry slot -1 and an empty context, so replays never write
-        stale slots.  Capture failure falls back to eager decode."""
+        stale slots.  Buckets of 128 and more get a second graph with the
+        whole-unit attention schedule (no merge launches), replayed when the
+        step's contexts are near-equal.  Capture failure falls back to eager
+        decode."""
         bufs = self._graph_bufs
         max_bs = bufs["input_ids"].shape[0]
+        sizes = sorted((b for b in batch_sizes if b <= max_bs), reverse=True)
+        plan = [(bs, 0) for bs in sizes] + [(bs, -1) for bs in sizes if bs >= UNIT_GRAPH_MIN_BS]
         try:
             with torch.no_grad():
-                for bs in sorted((b for b in batch_sizes if b <= max_bs), reverse=True):
+                for bs, pps in plan:
+                    self._set_decode_schedule(pps)
                     args = (bufs["input_ids"][:bs], bufs["positions"][:bs],
                             bufs["context_lens"][:bs], bufs["block_tables"][:bs],
                             bufs["slot_mapping"][:bs])
@@ -451,12 +472,15 @@ class Qwen3ForCausalLM(nn.Module):
                         bufs["outputs"][:bs] = self.model.forward_decode(*args)
                     if self._graph_pool is None:
                         self._graph_pool = graph.pool()
-                    self._graphs[bs] = graph
+                    (self._graphs_units if pps else self._graphs)[bs] = graph
             self._has_cuda_graphs = True
         except Exception as e:  # pragma: no cover - depends on the runtime
             print(f"HIP graph capture failed, decoding eagerly: {e}")
             self._graphs = {}
+            self._graphs_units = {}
             self._has_cuda_graphs = False
+        finally:
+            self._set_decode_schedule(0)
 
     def _run_decode_graph(self, bs, input_ids, positions, context_lens, block_tables,
                           slot_mapping):
@@ -502,7 +526,8 @@ class Qwen3ForCausalLM(nn.Module):
         self._graph_in.copy_(host, non_blocking=True)
         if ids_dev is not None:
             bufs["input_ids"][:bs].copy_(ids_dev)
-        self._graphs[graph_bs].replay()
+        graph = self._graphs_units.get(graph_bs) if near_equal_contexts(ctx[:graph_bs]) else None
+        (graph or self._graphs[graph_bs]).replay()
         return bufs["outputs"][:bs]
 
     # ---------------- step preparation (qwen3_naive.py:1147-1225) ----------------

@@ -217,10 +217,11 @@ def test_decode_misaligned_q_view(pkg, gpu):
     _check(out, w)
 
 
-def _decode_with_mode(pkg, gpu, w):
-    """Balanced schedule through the C ABI with an explicit workspace; returns
-    (out, unit_mode) where unit_mode is the mode word the split kernel
-    publishes as the last int32 of its workspace."""
+def _decode_with_mode(pkg, gpu, w, pps=0):
+    """Balanced schedule (``pps`` 0, or -1 for its whole-unit form) through
+    the C ABI with an explicit workspace and an output prefilled with 7s;
+    returns (out, unit_mode) where unit_mode is the mode word the split
+    kernel publishes as the last int32 of its workspace."""
     L = pkg._lib.lib()
     q = w["q"].to(gpu)
     kc, vc = w["k_cache"].to(gpu), w["v_cache"].to(gpu)
@@ -228,13 +229,13 @@ def _decode_with_mode(pkg, gpu, w):
     bt = w["block_tables"].to(gpu)
     bsz, hq, d = q.shape
     nb, _, hkv, _ = kc.shape
-    out = torch.empty_like(q)
-    nbytes = L.qmi_paged_decode_workspace_bytes(bsz, hkv, hq, bt.shape[1], 0)
+    out = torch.full_like(q, 7.0)
+    nbytes = L.qmi_paged_decode_workspace_bytes(bsz, hkv, hq, bt.shape[1], pps)
     ws = torch.zeros(nbytes // 4, dtype=torch.int32, device=gpu)
     st = L.qmi_paged_decode_attention(
         q.data_ptr(), q.stride(0), q.stride(1), kc.data_ptr(), vc.data_ptr(), nb, 256, hq, hkv,
         d, lens.data_ptr(), 0, bt.data_ptr(), bt.stride(0), bt.shape[1], bsz, w["scale"],
-        out.data_ptr(), out.stride(0), out.stride(1), ws.data_ptr(), nbytes, 0,
+        out.data_ptr(), out.stride(0), out.stride(1), ws.data_ptr(), nbytes, pps,
         torch.cuda.current_stream(gpu).cuda_stream)
     pkg._lib.check(st, "paged_decode_attention")
     torch.cuda.synchronize()
@@ -254,6 +255,33 @@ def test_decode_unit_mode_near_equal_lengths(pkg, gpu, bsz, hq, hkv):
     out, mode = _decode_with_mode(pkg, gpu, w)
     assert mode == 1
     assert out[[3, bsz - 1]].abs().max().item() == 0.0
+    _check(out, w)
+
+
+@pytest.mark.parametrize("lens_kind,bsz,hq,hkv", [
+    ("config1", 4, 16, 8), ("ragged", 64, 16, 8), ("equal", 256, 16, 8), ("ragged", 256, 16, 8),
+    ("equal", 128, 16, 4), ("equal", 300, 32, 16), ("empty", 130, 16, 8)])
+def test_decode_whole_units_forced(pkg, gpu, lens_kind, bsz, hq, hkv):
+    """pages_per_split = -1: one whole (sequence, head group) unit per
+    workgroup and no merge launch.  Exact for any lengths (ragged ones only
+    balance worse); empty sequences are written as zeros by the split."""
+    g = torch.Generator().manual_seed(70 + bsz + hkv)
+    if lens_kind == "config1":
+        lens = [38, 257, 301, 701]
+    elif lens_kind == "equal":
+        lens = torch.randint(600, 641, (bsz,), generator=g).tolist()
+    elif lens_kind == "empty":
+        lens = [0] * bsz
+    else:
+        lens = torch.randint(1, 1500, (bsz,), generator=g).tolist()
+    if lens_kind != "config1":
+        lens[1] = lens[bsz - 1] = 0
+    w = _ragged(71 + bsz, lens, hq=hq, hkv=hkv)
+    print(f"[decode] whole units {lens_kind} B={bsz} {hq}/{hkv}", flush=True)
+    out, mode = _decode_with_mode(pkg, gpu, w, pps=-1)
+    assert mode == 1
+    if lens_kind != "config1":
+        assert out[[1, bsz - 1]].abs().max().item() == 0.0
     _check(out, w)
 
 

@@ -2,6 +2,8 @@
 call surface, checked against the CPU oracle forward (fp32) and for the
 chunked / prefix-cache / decode self-consistency the reference's own tests
 assert (top-1 equal, top-20 overlap)."""
+import sys
+
 import pytest
 import torch
 
@@ -166,6 +168,52 @@ def test_graph_decode_equals_eager(pkg, model):
         assert (first.float() - eager.float()).abs().max().item() < 5e-2
     model._has_cuda_graphs = False
     model._graphs = {}
+
+
+class _ReplaySpy:
+    def __init__(self, graph):
+        self.graph, self.calls = graph, 0
+
+    def replay(self):
+        self.calls += 1
+        self.graph.replay()
+
+
+def test_graph_decode_whole_units(pkg, model, monkeypatch):
+    """Near-equal contexts replay the bucket's whole-unit graph (attention
+    without merge launches), ragged ones the balanced graph; both match eager."""
+    eng = sys.modules[type(model).__module__]
+    monkeypatch.setattr(eng, "UNIT_GRAPH_MIN_BS", 4)
+    g = torch.Generator().manual_seed(8)
+    print("[model] whole-unit decode graphs", flush=True)
+    with torch.no_grad():
+        model._init_cuda_graphs(max_bs=8, bt_width=4)
+        model._capture_decode_graphs(batch_sizes=(4, 8))
+        assert model._has_cuda_graphs and set(model._graphs_units) == {4, 8}
+        spy = _ReplaySpy(model._graphs_units[4])
+        model._graphs_units[4] = spy
+        for lens, units in (((300, 305, 310, 296), 1), ((40, 700, 300, 5), 0)):
+            bm = pkg.BlockManager(64)
+            seqs = []
+            for n in lens:
+                s = pkg.Sequence(torch.randint(0, VOCAB, (n,), generator=g).tolist())
+                bm.allocate(s)
+                _prefill(pkg, model, s, n)
+                s.append_token(9)
+                bm.may_append(s)
+                seqs.append(s)
+            ids, pos, ctx, bt, slot = model._prepare_decode(seqs)
+            eager = model.model.forward_decode(ids, pos, ctx, bt, slot).clone()
+            calls = spy.calls
+            out = model._run_decode_graph_seqs(seqs).clone()
+            torch.cuda.synchronize()
+            assert spy.calls - calls == units
+            assert (out.float() - eager.float()).abs().max().item() < 5e-2
+            for s in seqs:
+                bm.deallocate(s.block_table)
+    model._has_cuda_graphs = False
+    model._graphs = {}
+    model._graphs_units = {}
 
 
 def test_generate_continuous_and_logprobs(pkg, model):

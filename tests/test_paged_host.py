@@ -242,3 +242,18 @@ def test_scheduler_lifo_preemption():
     assert list(waiting) == [b] and b.status == "WAITING"
     assert b.kv_len == 0 and b.token_ids == list(range(300, 556)) and not b.block_table
     assert len(a.block_table) == 2 and eng._preemptions == 1
+
+
+
+def test_near_equal_contexts():
+    """Whole-unit decode when every key count (context + 1) is within 10% of
+    the rows' mean, padding rows included."""
+    near = paged.near_equal_contexts
+    assert near(np.array([600, 620, 640], dtype=np.int32))
+    assert near(np.array([639] * 5, dtype=np.int32))
+    assert not near(np.array([0, 10], dtype=np.int32))          # 11 keys vs mean 6
+    assert not near(np.array([600] * 3 + [0], dtype=np.int32))  # a padding row
+    # 10 * max * n <= 11 * sum: keys (100, 120) give 2400 <= 2420
+    assert near(np.array([99, 119], dtype=np.int32))
+    assert not near(np.array([99, 122], dtype=np.int32))        # 2460 > 2442
+    assert not near(np.array([], dtype=np.int32))
