@@ -285,10 +285,11 @@ int qmi_ppo_clipped_loss(const float* new_lp, const float* old_lp, const float* 
  * contiguous; rewards fp32 [n_seq]; prompt_ids int64 [n_seq].
  * Outputs: out_lp, out_lse fp32 [n_seq, n_tok]; out_adv fp32 [n_seq];
  * out_dlp fp32 [n_seq, n_tok] (d loss / d lp); out_loss fp32 scalar.
- * workspace: qmi_grpo_fused_workspace_bytes(n_seq, n_tok) bytes (arrival
- * counters and per-sequence sums), zeroed by the caller once before first
- * use; the kernel leaves its counters at zero again when it completes, so
- * calls on one stream can reuse it.  Concurrent calls must not share one.
+ * workspace: qmi_grpo_fused_workspace_bytes(n_seq, n_tok) bytes, 16-byte
+ * aligned (per-sequence sums; no initial contents needed, nothing kept
+ * between calls).  Concurrent calls must not share one.
+ * Launches: the row pass, one workgroup per sequence for the loss terms,
+ * and one more small launch that applies the token-mean denominator.
  */
 int64_t qmi_grpo_fused_workspace_bytes(int64_t n_seq, int64_t n_tok);
 

@@ -15,11 +15,13 @@
 // The pairs are merged with shuffles and one LDS exchange.  Row workgroups
 // use no fences or atomics: an agent-scope fence on gfx950 writes back and
 // invalidates the L2, which costs more than the row itself when 16K
-// workgroups each issue one.  The loss therefore runs as a second, tiny
-// launch with one workgroup per sequence (advantage, token losses and their
-// gradients), whose last arrival computes the scalar.  All sums run in a
-// fixed order, so results are deterministic; the arrival counter is reset by
-// the finisher.
+// workgroups each issue one.  The loss therefore runs as two more tiny
+// launches: one workgroup per sequence computes the advantage, token losses,
+// their gradients and the sequence's sums (each reads its own mask row
+// once), then one workgroup per sequence applies the token-mean
+// denominator (the sum of the per-sequence mask sums) to its gradients while
+// workgroup 0 writes the scalar.  All sums run in a fixed order, so results
+// are deterministic, and the workspace holds no state between calls.
 #include "qmi_common.h"
 
 namespace {
@@ -180,7 +182,6 @@ __global__ __launch_bounds__(kThreads) void logprob_rows(
 }
 
 struct FusedWs {
-  uint32_t* all_count;   // [1]     sequences that have finished
   float* seq_sum;        // [n_seq] sum_t l*m
   float* seq_msum;       // [n_seq] sum_t m
 };
@@ -188,14 +189,12 @@ struct FusedWs {
 __host__ __device__ inline int64_t align16(int64_t x) { return (x + 15) & ~(int64_t)15; }
 
 __host__ __device__ inline int64_t fused_ws_bytes(int64_t n_seq) {
-  return align16(4) + 2 * align16(4 * n_seq);
+  return 2 * align16(4 * n_seq);
 }
 
 __device__ inline FusedWs fused_ws(void* base, int64_t n_seq) {
   char* p = reinterpret_cast<char*>(base);
   FusedWs w;
-  w.all_count = reinterpret_cast<uint32_t*>(p);
-  p += align16(4);
   w.seq_sum = reinterpret_cast<float*>(p);
   p += align16(4 * n_seq);
   w.seq_msum = reinterpret_cast<float*>(p);
@@ -241,29 +240,20 @@ __device__ float block_group_advantage(const float* __restrict__ rewards,
   return (rewards[i] - mean) / (sqrtf(ss / (cnt - 1.f)) + eps);
 }
 
-__device__ __forceinline__ uint32_t arrive(uint32_t* counter) {
-  return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ void reset_counter(uint32_t* counter) {
-  __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Loss epilogue of the fused step, launched right after logprob_rows has
-// written lp for every row (the kernel boundary orders the two, so the row
-// workgroups need no fences or atomics).  One workgroup per sequence b: the
-// group advantage of b, the masked token losses and their gradients for the
-// n_tok tokens of b, and b's sums.  The last sequence to finish (an arrival
-// counter; n_seq fences in total) computes the scalar loss.  Every reduction
-// runs in a fixed order, so the result is deterministic.
+// Loss epilogue of the fused step, part 1, launched right after
+// logprob_rows has written lp for every row (the kernel boundary orders the
+// two).  One workgroup per sequence b: the group advantage of b, the masked
+// token losses and their gradients d loss / d lp for the n_tok tokens of b,
+// and b's sums sum_t l*m and sum_t m.  Per-sequence mean: the gradients are
+// final here (denominator n_seq * (sum_t m + 1e-8)).  Token mean: they are
+// written without the denominator, which part 2 applies.
 __global__ __launch_bounds__(kThreads) void grpo_loss_seqs(
     const float* __restrict__ lp, const float* __restrict__ old_lp,
     const float* __restrict__ mask, const float* __restrict__ rewards,
     const int64_t* __restrict__ prompt_ids, int64_t n_seq, int64_t n_tok, float adv_eps,
     float clip, int reduction, float* __restrict__ out_adv, float* __restrict__ out_dlp,
-    float* __restrict__ out_loss, void* __restrict__ ws_base) {
+    void* __restrict__ ws_base) {
   __shared__ float sm_red[kWaves];
-  __shared__ bool sm_last;
   const FusedWs ws = fused_ws(ws_base, n_seq);
   const int64_t b = blockIdx.x;
   const float adv = block_group_advantage(rewards, prompt_ids, n_seq, b, adv_eps, sm_red);
@@ -272,46 +262,50 @@ __global__ __launch_bounds__(kThreads) void grpo_loss_seqs(
   for (int64_t j = threadIdx.x; j < n_tok; j += kThreads) {
     const float m = mask[base + j];
     smk += m;
-    if (m != 0.f) {
-      float l, g;
-      ppo_token(lp[base + j], old_lp[base + j], adv, clip, &l, &g);
-      sl += l * m;
-    }
-  }
-  sl = block_sum(sl, sm_red);
-  smk = block_sum(smk, sm_red);
-  float den;
-  if (reduction == QMI_REDUCE_TOKEN_MEAN) {
-    float all = 0.f;
-    for (int64_t j = threadIdx.x; j < n_seq * n_tok; j += kThreads) all += mask[j];
-    den = block_sum(all, sm_red) + 1e-8f;
-  } else {
-    den = (float)n_seq * (smk + 1e-8f);
-  }
-  const float inv = 1.0f / den;
-  for (int64_t j = threadIdx.x; j < n_tok; j += kThreads) {
-    const float m = mask[base + j];
     float g = 0.f;
     if (m != 0.f) {
       float l;
       ppo_token(lp[base + j], old_lp[base + j], adv, clip, &l, &g);
-      g *= m * inv;
+      sl += l * m;
+      g *= m;
     }
     out_dlp[base + j] = g;
+  }
+  sl = block_sum(sl, sm_red);
+  smk = block_sum(smk, sm_red);
+  if (reduction == QMI_REDUCE_SEQ_MEAN) {
+    const float inv = 1.0f / ((float)n_seq * (smk + 1e-8f));
+    for (int64_t j = threadIdx.x; j < n_tok; j += kThreads) out_dlp[base + j] *= inv;
   }
   if (threadIdx.x == 0) {
     ws.seq_sum[b] = sl;
     ws.seq_msum[b] = smk;
     out_adv[b] = adv;
-    __threadfence();
-    sm_last = (arrive(ws.all_count) == (uint32_t)(n_seq - 1));
   }
-  __syncthreads();
-  if (!sm_last) return;
+}
 
-  // ---- last sequence: the scalar loss in sequence order ----
-  __threadfence();
-  if (threadIdx.x == 0) {
+// Part 2.  Token mean: workgroup b scales sequence b's gradients by
+// 1 / (sum of every sequence's mask sum + 1e-8), each workgroup forming that
+// sum in the same fixed order.  Workgroup 0 also writes the scalar loss
+// (sequence order).  Launched with n_seq workgroups for the token mean and
+// one for the per-sequence mean.
+__global__ __launch_bounds__(kThreads) void grpo_loss_finish(int64_t n_seq, int64_t n_tok,
+                                                             int reduction,
+                                                             float* __restrict__ out_dlp,
+                                                             float* __restrict__ out_loss,
+                                                             const void* __restrict__ ws_base) {
+  __shared__ float sm_red[kWaves];
+  const FusedWs ws = fused_ws(const_cast<void*>(ws_base), n_seq);
+  const int64_t b = blockIdx.x;
+  if (reduction == QMI_REDUCE_TOKEN_MEAN) {
+    float part = 0.f;
+    for (int64_t j = threadIdx.x; j < n_seq; j += kThreads) part += ws.seq_msum[j];
+    const float den = block_sum(part, sm_red) + 1e-8f;
+    const float inv = 1.0f / den;
+    const int64_t base = b * n_tok;
+    for (int64_t j = threadIdx.x; j < n_tok; j += kThreads) out_dlp[base + j] *= inv;
+  }
+  if (b == 0 && threadIdx.x == 0) {
     float loss;
     if (reduction == QMI_REDUCE_TOKEN_MEAN) {
       float num = 0.f, msum = 0.f;
@@ -326,7 +320,6 @@ __global__ __launch_bounds__(kThreads) void grpo_loss_seqs(
       loss = acc / (float)n_seq;
     }
     *out_loss = loss;
-    reset_counter(ws.all_count);
   }
 }
 
@@ -550,7 +543,12 @@ extern "C" int qmi_grpo_fused_loss(const uint16_t* logits, int64_t lss, int64_t 
   if (e != hipSuccess) return (int)e;
   hipLaunchKernelGGL(grpo_loss_seqs, dim3((unsigned)n_seq), dim3(kThreads), 0, s, out_lp, old_lp,
                      mask, rewards, prompt_ids, n_seq, n_tok, adv_eps, clip_eps, (int)reduction,
-                     out_adv, out_dlp, out_loss, workspace);
+                     out_adv, out_dlp, workspace);
+  e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  const unsigned fin = reduction == QMI_REDUCE_TOKEN_MEAN ? (unsigned)n_seq : 1u;
+  hipLaunchKernelGGL(grpo_loss_finish, dim3(fin), dim3(kThreads), 0, s, n_seq, n_tok,
+                     (int)reduction, out_dlp, out_loss, workspace);
   QMI_RETURN_LAUNCH_STATUS();
 }
 

@@ -519,25 +519,6 @@ def ppo_clipped_loss_fwd(new_lp: torch.Tensor, old_lp: torch.Tensor, adv: torch.
     return loss, dlp
 
 
-_FUSED_WS: dict[tuple[int, int], torch.Tensor] = {}
-
-
-def _fused_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Cached zero-initialised workspace per (device, stream).
-
-    The fused kernel leaves its arrival counters at zero when it finishes, so
-    the buffer is zeroed only when it is (re)allocated.  Calls on the same
-    stream are ordered; calls on different streams get different buffers.
-    """
-    key = (device.index if device.index is not None else torch.cuda.current_device(),
-           stream_handle(device))
-    ws = _FUSED_WS.get(key)
-    if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(((nbytes + 15) // 16) * 16, dtype=torch.uint8, device=device)
-        _FUSED_WS[key] = ws
-    return ws
-
-
 def grpo_fused_forward(logits: torch.Tensor, ids: torch.Tensor, old_lp: torch.Tensor,
                        mask: torch.Tensor, rewards: torch.Tensor, prompt_ids: torch.Tensor,
                        adv_eps: float = 1e-8, clip_eps: float = 0.2, reduction: str = "token"):
@@ -561,7 +542,8 @@ def grpo_fused_forward(logits: torch.Tensor, ids: torch.Tensor, old_lp: torch.Te
     loss = torch.empty((), dtype=torch.float32, device=dev)
     L = lib()
     nbytes = L.qmi_grpo_fused_workspace_bytes(bsz, t)
-    ws = _fused_workspace(dev, nbytes)
+    # Per-sequence sums only; the kernels keep no state in it between calls.
+    ws = torch.empty(((nbytes + 15) // 16) * 16, dtype=torch.uint8, device=dev)
     check(L.qmi_grpo_fused_loss(lg.data_ptr(), lg.stride(0), lg.stride(1), ii.data_ptr(),
                                 ii.stride(0), ii.stride(1), bsz, t, v, od.data_ptr(),
                                 mk.data_ptr(), rw.data_ptr(), pid.data_ptr(), float(adv_eps),

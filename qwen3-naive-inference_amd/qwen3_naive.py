@@ -527,6 +527,8 @@ class Qwen3ForCausalLM(nn.Module):
         if ids_dev is not None:
             bufs["input_ids"][:bs].copy_(ids_dev)
         graph = self._graphs_units.get(graph_bs) if near_equal_contexts(ctx[:graph_bs]) else None
+        if graph is not None and isinstance(getattr(self, "last_stats", None), dict):
+            self.last_stats["unit_graph_steps"] = self.last_stats.get("unit_graph_steps", 0) + 1
         (graph or self._graphs[graph_bs]).replay()
         return bufs["outputs"][:bs]
 
@@ -651,7 +653,8 @@ class Qwen3ForCausalLM(nn.Module):
         all_seqs = list(waiting)
         running: list[Sequence] = []
         self._preemptions = 0
-        self.last_stats = {"steps": 0, "decode_steps": 0, "graph_steps": 0, "lookahead_steps": 0}
+        self.last_stats = {"steps": 0, "decode_steps": 0, "graph_steps": 0, "unit_graph_steps": 0,
+                           "lookahead_steps": 0}
         dev = self._device()
         # Decode lookahead: without EOS a sequence finishes by count alone, so
         # the host can launch decode step t+1 (its input ids gathered on the
@@ -686,8 +689,14 @@ class Qwen3ForCausalLM(nn.Module):
             if all_decode and lookahead:
                 ids_dev = None
                 if pending is not None:
+                    # A row takes its input id from the previous step's samples
+                    # only while its last token is still that placeholder: a
+                    # sequence preempted and re-admitted in the same round (a
+                    # one-token prefill remainder) was rolled back to its prompt
+                    # and must be fed its last prompt token from the host.
                     rows = pending["row_of"]
-                    idx = [rows.get(id(s), -1) for s in scheduled]
+                    idx = [rows.get(id(s), -1) if s.last_token == _PENDING_TOKEN else -1
+                           for s in scheduled]
                     if min(idx) < 0:
                         flush()
                     elif idx == list(range(pending["n"])):

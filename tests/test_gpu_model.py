@@ -16,7 +16,11 @@ LAYERS, VOCAB = 2, 2048
 
 @pytest.fixture(scope="module")
 def model(pkg, gpu):
-    cfg = pkg.Qwen3Config(num_hidden_layers=LAYERS, vocab_size=VOCAB)
+    # Untied lm_head: with a tied random embedding the residual stream keeps
+    # the input token's own embedding, which then takes p ~ 1 and makes every
+    # sampled log-probability ~0.  N(0, 0.1) gives logits of std ~3 over the
+    # 2,048-token vocabulary: peaked but with entropy left to sample from.
+    cfg = pkg.Qwen3Config(num_hidden_layers=LAYERS, vocab_size=VOCAB, tie_word_embeddings=False)
     torch.manual_seed(0)
     m = pkg.Qwen3ForCausalLM(cfg)
     with torch.no_grad():
@@ -24,7 +28,9 @@ def model(pkg, gpu):
             if "norm" in name:
                 p.uniform_(0.8, 1.2)
             elif "embed" in name:
-                p.normal_(0, 0.25)              # tied lm_head: logits O(5)
+                p.normal_(0, 0.25)
+            elif "lm_head" in name:
+                p.normal_(0, 0.1)
             elif p.dim() == 2:
                 p.normal_(0, 0.02)
     m = m.to(gpu).to(torch.bfloat16).eval()
@@ -216,6 +222,46 @@ def test_graph_decode_whole_units(pkg, model, monkeypatch):
     model._graphs_units = {}
 
 
+def _oracle_logprobs(model, toks, plen, n_layers=LAYERS, mode="fp32"):
+    """Oracle log-probabilities of the generated tokens toks[plen:], each
+    scored at the previous position (temperature 1, no top-k: the sampling
+    distribution of generate_continuous_with_logprobs, qwen3_naive.py:1636-1650)."""
+    logits = OM.qwen3_logits(model.state_dict(), torch.as_tensor(toks[:-1])[None], n_layers,
+                             mode=mode)[0]
+    lp = torch.log_softmax(logits.double(), -1)
+    tgt = torch.as_tensor(toks[plen:])
+    return lp[plen - 1:].gather(-1, tgt[:, None])[:, 0]
+
+
+# Log-probability bounds, 2x the measured deviation, against the oracle in the
+# reference's bf16 numerics and against the exact fp32 oracle.  The deviation is
+# set by the bf16 rounding of the logits (the reference's lm_head output is
+# bf16 too): half an ulp is 1/32 nat at |x| in [8, 16), and a sampled token's
+# logit and the top logits that dominate the log-sum-exp each carry one; the
+# bf16 oracle rounds at the same points, but fp32 values that differ slightly
+# upstream round to neighbouring bf16 values now and then (one full ulp).
+LP_BF16_MAX, LP_BF16_MEAN = 0.12, 0.03
+LP_FP32_MAX, LP_FP32_MEAN = 0.12, 0.035
+
+
+def _assert_logprobs_match_oracle(model, toks, lps, plens, n_layers=LAYERS, rows=None, tag=""):
+    """Engine log-probs against the oracle teacher-forced on the engine's own
+    tokens, in both oracle modes."""
+    d16, d32 = [], []
+    for b in (range(len(toks)) if rows is None else rows):
+        got = torch.tensor(lps[b], dtype=torch.float64)
+        for mode, acc in (("bf16", d16), ("fp32", d32)):
+            ref = _oracle_logprobs(model, toks[b], plens[b], n_layers, mode)
+            assert got.shape == ref.shape
+            acc.append((got - ref).abs())
+    d16, d32 = torch.cat(d16), torch.cat(d32)
+    print(f"[model] {tag} log-prob |engine - oracle| over {d16.numel()} tokens: "
+          f"bf16 oracle max {d16.max().item():.5f} mean {d16.mean().item():.6f}; "
+          f"fp32 oracle max {d32.max().item():.5f} mean {d32.mean().item():.6f}", flush=True)
+    assert d16.max().item() <= LP_BF16_MAX and d16.mean().item() <= LP_BF16_MEAN
+    assert d32.max().item() <= LP_FP32_MAX and d32.mean().item() <= LP_FP32_MEAN
+
+
 def test_generate_continuous_and_logprobs(pkg, model):
     g = torch.Generator().manual_seed(6)
     prompts = [torch.randint(0, VOCAB, (1, n), generator=g) for n in (20, 300, 77)]
@@ -229,19 +275,46 @@ def test_generate_continuous_and_logprobs(pkg, model):
     toks, gen2, lps, plens = model.generate_continuous_with_logprobs(
         prompts, max_new_tokens=12, temperature=1.0, top_k=None)
     assert plens == [20, 300, 77] and [len(x) for x in lps] == [12, 12, 12]
-    # Old log-probs equal the log-softmax of the model's own logits at the
-    # previous position (teacher-forced recomputation through prefill).
-    bm = pkg.BlockManager(64)
-    for b in range(3):
-        s = pkg.Sequence(toks[b][:-1])
-        bm.allocate(s)
-        logits = _prefill(pkg, model, s, len(toks[b]) - 1)
-        lp = torch.log_softmax(logits, -1)
-        tgt = torch.tensor(toks[b][plens[b]:], device=lp.device)
-        re = lp[plens[b] - 1:].gather(-1, tgt[:, None])[:, 0].cpu()
-        d = (re - torch.tensor(lps[b])).abs()
-        assert d.max().item() < 0.25 and d.median().item() < 0.05
-        bm.deallocate(s.block_table)
+    assert gen2 == gen                      # same seed, same tokens with or without log-probs
+    _assert_logprobs_match_oracle(model, toks, lps, plens, tag="graphs+lookahead")
+
+
+@pytest.mark.parametrize("mode", ["balanced_graph", "unit_graph", "eager", "lookahead"])
+def test_engine_logprobs_match_oracle(pkg, model, monkeypatch, mode):
+    """Every decode mode of the engine returns the log-probabilities the fp32
+    oracle gives for the engine's own tokens: the balanced-schedule graphs
+    (ragged contexts), the whole-unit graphs (near-equal contexts), eager
+    decode, and the one-step lookahead."""
+    eng = sys.modules[type(model).__module__]
+    g = torch.Generator().manual_seed(21)
+    if mode == "unit_graph":
+        monkeypatch.setattr(eng, "UNIT_GRAPH_MIN_BS", 4)
+        lens = (300, 305, 310, 296)
+    else:
+        lens = (20, 300, 77, 513)
+    prompts = [torch.randint(0, VOCAB, (1, n), generator=g) for n in lens]
+    model._has_cuda_graphs = False
+    model.decode_lookahead = mode == "lookahead"
+    try:
+        torch.manual_seed(5)
+        print(f"[model] engine vs oracle: {mode}", flush=True)
+        toks, _, lps, plens = model.generate_continuous_with_logprobs(
+            prompts, max_new_tokens=24, temperature=1.0, top_k=None, use_graphs=mode != "eager")
+        st = model.last_stats
+        if mode == "eager":
+            assert st["graph_steps"] == 0
+        else:
+            assert st["graph_steps"] > 0
+        if mode == "unit_graph":
+            assert st["unit_graph_steps"] > 0
+        if mode == "balanced_graph":
+            assert st["unit_graph_steps"] == 0
+        assert (st["lookahead_steps"] > 0) == (mode == "lookahead")
+        _assert_logprobs_match_oracle(model, toks, lps, plens, tag=mode)
+    finally:
+        model.decode_lookahead = True
+        model._has_cuda_graphs = False
+        model._graphs, model._graphs_units = {}, {}
 
 
 def test_generation_with_preemption(pkg, model):
@@ -269,6 +342,10 @@ def test_decode_lookahead_matches_synchronous_engine(pkg, model, graphs, blocks)
     g = torch.Generator().manual_seed(8)
     # Four ~250-token prompts + 40 tokens need 8 pages at the end: 6 forces preemption.
     prompts = [torch.randint(0, VOCAB, (1, n), generator=g) for n in (250, 240, 251, 245)]
+    _lookahead_vs_sync(model, prompts, 40, graphs, blocks)
+
+
+def _lookahead_vs_sync(model, prompts, new_tokens, graphs, blocks, oracle_rows=None):
     if blocks is not None:
         model.allocate_global_kv_cache(num_blocks=blocks)
     try:
@@ -277,19 +354,37 @@ def test_decode_lookahead_matches_synchronous_engine(pkg, model, graphs, blocks)
             model.decode_lookahead = la
             torch.manual_seed(3)
             print(f"[model] lookahead={la} graphs={graphs} blocks={blocks}", flush=True)
-            out = model.generate_continuous_with_logprobs(prompts, max_new_tokens=40,
+            out = model.generate_continuous_with_logprobs(prompts, max_new_tokens=new_tokens,
                                                           temperature=1.0, top_k=None,
                                                           use_graphs=graphs)
             runs.append((out, dict(model.last_stats)))
-        (t0, _, l0, _), s0 = runs[0]
+        (t0, _, l0, p0), s0 = runs[0]
         (t1, _, l1, _), s1 = runs[1]
         assert t0 == t1 and l0 == l1
         assert all(t >= 0 for seq in t1 for t in seq)
         assert s1["lookahead_steps"] > 0 and s0["lookahead_steps"] == 0
         if blocks is not None:
             assert s1["preemptions"] > 0 and s1["preemptions"] == s0["preemptions"]
+        if oracle_rows is not None:
+            _assert_logprobs_match_oracle(model, t1, l1, p0, rows=oracle_rows,
+                                          tag="lookahead after preemption")
     finally:
         model.decode_lookahead = True
         if blocks is not None:
             model._num_blocks = 0
             model.allocate_global_kv_cache(num_blocks=64)
+
+
+@pytest.mark.parametrize("prompt_len", [1, 257])
+def test_lookahead_readmitted_victim(pkg, model, prompt_len):
+    """A victim preempted and re-admitted in the same scheduling round with a
+    one-token prefill remainder (a one-token prompt, or a 257-token prompt
+    whose first page is a prefix-cache hit) joins an all-decode step; the
+    lookahead must feed it its last prompt token, not the token it sampled
+    before it was rolled back.  Two sequences in a 5-page pool: at 512 tokens
+    the second is its own LIFO victim, frees two pages and comes straight
+    back."""
+    g = torch.Generator().manual_seed(30 + prompt_len)
+    prompts = [torch.randint(0, VOCAB, (1, prompt_len), generator=g) for _ in range(2)]
+    new_tokens = 600 - prompt_len
+    _lookahead_vs_sync(model, prompts, new_tokens, True, 5, oracle_rows=[1])

@@ -132,19 +132,26 @@ def test_prefill_chunked_equals_unchunked(pkg, gpu):
     _check(full, q, kc, vc, [0, L], [0, L], bt)
 
 
-def test_prefill_config4_step(pkg, gpu):
-    """First chunk step of the prefix-cache workload: 16 sequences, 512 cached
-    prefix tokens in 2 shared pages, 512-token chunks (8,192 query rows)."""
-    sched = W.prefix_prefill_chunks(seed=0)
-    step = sched["steps"][0]
+_CONFIG4 = W.prefix_prefill_chunks(seed=0)
+
+
+@pytest.mark.parametrize("step_idx", range(len(_CONFIG4["steps"])))
+def test_prefill_config4_step(pkg, gpu, step_idx):
+    """Every chunk step of the prefix-cache workload: 16 sequences, 512 cached
+    prefix tokens in 2 shared pages, 512-token chunks.  Step 1 has 8,192 query
+    rows; the later steps carry the longest key ranges (up to 2,560 keys),
+    fewer sequences and the launch tails.  Every sequence of the step is
+    compared with the oracle."""
+    step = _CONFIG4["steps"][step_idx]
     n_blocks = 2 + 16 * 16
     inp = W.prefill_step_inputs(0, step, [0, 1], n_blocks)
     g = torch.Generator().manual_seed(15)
     kc = torch.randn(n_blocks, 256, 8, 128, generator=g).to(torch.bfloat16)
     vc = torch.randn(n_blocks, 256, 8, 128, generator=g).to(torch.bfloat16)
-    print("[prefill] config4 step", flush=True)
     cu_q = inp["cu_seqlens_q"].tolist()
     cu_k = inp["cu_seqlens_k"].tolist()
+    print(f"[prefill] config4 step {step_idx + 1}/{len(_CONFIG4['steps'])}: {len(step)} seqs, "
+          f"{cu_q[-1]} queries, max keys {inp['max_seqlen_k']}", flush=True)
     out = _run(pkg, gpu, inp["q"], kc, vc, cu_q, cu_k, inp["block_tables"])
     _check(out, inp["q"], kc, vc, cu_q, cu_k, inp["block_tables"])
 

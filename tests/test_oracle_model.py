@@ -91,3 +91,80 @@ def test_product_cpu_forward_matches_oracle():
         got = model(ids)
     ref = OM.qwen3_logits(model.state_dict(), ids, 2)
     torch.testing.assert_close(got, ref, atol=2e-4, rtol=2e-4)
+
+
+def test_oracle_decode_step_continues_the_forward():
+    """Decoding token T-1 over the keys/values the forward left for positions
+    0..T-2 gives the forward's last-position logits (float64), for sequences
+    of different lengths in one batch; the returned new K/V rows are the
+    forward's rows at position T-1."""
+    hf, cfg = _hf_tiny()
+    sd = _fused_state_dict(hf)
+    args = (cfg.num_hidden_layers, cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim)
+    g = torch.Generator().manual_seed(6)
+    seqs = [torch.randint(0, cfg.vocab_size, (n,), generator=g) for n in (1, 9, 40)]
+    full, kctx, vctx, last, pos = [], [[] for _ in range(args[0])], [[] for _ in range(args[0])], [], []
+    fwd = []
+    for s in seqs:
+        logits, ks, vs = OM.qwen3_forward_kv(sd, s[None], *args, dtype=torch.float64)
+        fwd.append((logits[0, -1], [k[0, -1] for k in ks], [v[0, -1] for v in vs]))
+        for i in range(args[0]):
+            kctx[i].append(ks[i][0, :-1])
+            vctx[i].append(vs[i][0, :-1])
+        last.append(int(s[-1]))
+        pos.append(len(s) - 1)
+    logits, nk, nv, _ = OM.qwen3_decode_step(sd, last, pos, kctx, vctx, *args, dtype=torch.float64)
+    for b, (lg, k_last, v_last) in enumerate(fwd):
+        torch.testing.assert_close(logits[b], lg, atol=1e-10, rtol=1e-10)
+        for i in range(args[0]):
+            torch.testing.assert_close(nk[i, b], k_last[i], atol=1e-10, rtol=1e-10)
+            torch.testing.assert_close(nv[i, b], v_last[i], atol=1e-10, rtol=1e-10)
+    # A dropped cached row (or a wrong position) changes the result.
+    kbad = [[k[1:] if b == 2 else k for b, k in enumerate(kl)] for kl in kctx]
+    vbad = [[v[1:] if b == 2 else v for b, v in enumerate(vl)] for vl in vctx]
+    bad, _, _, _ = OM.qwen3_decode_step(sd, last, pos, kbad, vbad, *args, dtype=torch.float64)
+    assert not torch.allclose(bad[2], fwd[2][0], atol=1e-6)
+    bad2, _, _, _ = OM.qwen3_decode_step(sd, last, [p + 1 for p in pos], kctx, vctx, *args,
+                                         dtype=torch.float64)
+    assert not torch.allclose(bad2[1], fwd[1][0], atol=1e-6)
+
+
+def test_oracle_bf16_mode_tracks_transformers_bf16():
+    """The bf16 mode (the reference's bf16 rounding points) against an
+    independent bf16 implementation: transformers' Qwen3 run in bfloat16.
+    Both sit the same bf16 drift away from the exact fp32 logits, and the two
+    bf16 computations are much closer to each other than a formula error
+    (a dropped norm or a wrong RoPE pairing) would leave them."""
+    hf, cfg = _hf_tiny()
+    sd = _fused_state_dict(hf)
+    ids = torch.randint(0, cfg.vocab_size, (2, 37), generator=torch.Generator().manual_seed(7))
+    args = (cfg.num_hidden_layers, cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim)
+    sd16 = {k: v.to(torch.bfloat16) for k, v in sd.items()}
+    exact = OM.qwen3_logits(sd16, ids, *args, dtype=torch.float64)
+    ours = OM.qwen3_logits(sd16, ids, *args, mode="bf16")
+    hf16 = hf.to(torch.bfloat16)
+    with torch.no_grad():
+        theirs = hf16(ids).logits.float()
+    rel = lambda a, b: ((a.double() - b.double()).norm() / b.double().norm()).item()
+    d_ours, d_theirs, d_between = rel(ours, exact), rel(theirs, exact), rel(ours, theirs)
+    assert 1e-4 < d_ours < 3e-2 and d_theirs < 3e-2
+    assert d_between < 1.5e-2
+    assert d_ours < 2.5 * d_theirs + 1e-3
+
+
+def test_oracle_bf16_decode_step_continues_the_forward():
+    """In bf16 mode the decode step over the forward's cached rows gives the
+    forward's last-position logits up to one-ulp rounding flips (the one-row
+    and the batched GEMMs may round differently)."""
+    hf, cfg = _hf_tiny()
+    sd = {k: v.to(torch.bfloat16) for k, v in _fused_state_dict(hf).items()}
+    args = (cfg.num_hidden_layers, cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim)
+    s = torch.randint(0, cfg.vocab_size, (30,), generator=torch.Generator().manual_seed(8))
+    logits, ks, vs = OM.qwen3_forward_kv(sd, s[None], *args, mode="bf16")
+    kctx = [[k[0, :-1]] for k in ks]
+    vctx = [[v[0, :-1]] for v in vs]
+    step, nk, nv, _ = OM.qwen3_decode_step(sd, [int(s[-1])], [29], kctx, vctx, *args, mode="bf16")
+    rel = ((step[0] - logits[0, -1]).norm() / logits[0, -1].norm()).item()
+    assert rel < 1e-2
+    for i in range(args[0]):
+        assert ((nk[i, 0] - ks[i][0, -1]).norm() / ks[i][0, -1].norm()).item() < 1e-2
