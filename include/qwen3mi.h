@@ -30,6 +30,7 @@ extern "C" {
 #define QMI_E_BAD_STRIDE (-3)
 #define QMI_E_UNSUPPORTED (-4)
 #define QMI_E_WORKSPACE_TOO_SMALL (-5)
+#define QMI_E_SCRATCH_LIMIT (-6)
 
 /* Human-readable text for a return code of any entry point. */
 const char* qmi_error_string(int code);
@@ -104,6 +105,33 @@ int qmi_paged_decode_attention(const uint16_t* q, int64_t q_seq_stride, int64_t 
                                uint16_t* out, int64_t out_seq_stride, int64_t out_head_stride,
                                float* workspace, int64_t workspace_bytes,
                                int64_t pages_per_split, void* stream);
+
+/*
+ * Paged GQA decode attention that allocates nothing: no counterpart in the
+ * reference.  For callers that cannot allocate device memory or take a
+ * workspace (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Same arguments and results as
+ * qmi_paged_decode_attention without the workspace pair; the kernels use a
+ * 16 MiB static device array instead (one per device, held until the
+ * process ends; its address is looked up on the first call on a device, so
+ * make that first call outside a graph capture).  Problems whose
+ * qmi_paged_decode_workspace_bytes() exceeds 16 MiB are rejected with
+ * QMI_E_SCRATCH_LIMIT before anything is launched (Qwen3-0.6B's 16 / 8
+ * heads need 8.7 MB on 256 CUs at any batch up to 1024).  The array keeps
+ * the last call's contents and needs no clearing, but calls that overlap on
+ * one device share it and race: serialise them (one stream, or events).
+ */
+int qmi_paged_decode_attention_noalloc(const uint16_t* q, int64_t q_seq_stride,
+                                       int64_t q_head_stride, const uint16_t* k_cache,
+                                       const uint16_t* v_cache, int64_t num_blocks,
+                                       int64_t block_size, int64_t num_q_heads,
+                                       int64_t num_kv_heads, int64_t head_dim,
+                                       const int32_t* seqlens, int32_t seqlen_bias,
+                                       const int32_t* block_table, int64_t bt_stride,
+                                       int64_t bt_width, int64_t batch, float scale,
+                                       uint16_t* out, int64_t out_seq_stride,
+                                       int64_t out_head_stride, int64_t pages_per_split,
+                                       void* stream);
 
 /*
  * Varlen paged causal prefill attention (bf16 MFMA).

@@ -19,6 +19,9 @@ extern "C" const char* qmi_error_string(int code) {
       return "qwen3mi: unsupported configuration (head_dim, block size, GQA ratio or size limit)";
     case QMI_E_WORKSPACE_TOO_SMALL:
       return "qwen3mi: workspace missing or smaller than required";
+    case QMI_E_SCRATCH_LIMIT:
+      return "qwen3mi: problem needs more workspace than the library's static device scratch "
+             "holds (use the entry point that takes a workspace)";
     default:
       break;
   }

@@ -29,6 +29,9 @@
 //
 // All softmax arithmetic is fp32 in the log2 domain (exp2 with the scale
 // pre-multiplied by log2(e)).
+#include <atomic>
+#include <mutex>
+
 #include "qmi_common.h"
 
 namespace {
@@ -395,4 +398,79 @@ extern "C" int qmi_paged_decode_attention(
       return QMI_E_UNSUPPORTED;
   }
 #undef QMI_DECODE_CASE
+}
+
+// ---------------------------------------------------------------------------
+// No-allocation variant: the workspace is a file-scope device array instead
+// of a caller buffer.  Each device that loads the library holds its own copy
+// until the process ends; host code reaches it only through the address
+// hipGetSymbolAddress returns for that device (the array's name is a host
+// stand-in, not a device address).  Every workspace word the kernels read is
+// written earlier in the same call (partial slots by the split, the step
+// offsets and mode word by its workgroup 0), so nothing needs clearing
+// between calls.  Calls that overlap on one device share the array and race.
+namespace {
+
+constexpr int64_t kDecodeScratchBytes = 16ll << 20;
+__device__ __align__(256) float scratch[kDecodeScratchBytes / sizeof(float)];
+
+constexpr int kMaxScratchDevices = 64;
+std::atomic<float*> g_scratch_ptr[kMaxScratchDevices];
+std::mutex g_scratch_mu;
+
+// Device address of `scratch` on the calling thread's current device (the
+// device of the stream and of every pointer, as for all entry points),
+// looked up once per device with that device current.
+int decode_scratch(float** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxScratchDevices) return QMI_E_UNSUPPORTED;
+  float* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      void* addr = nullptr;
+      e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return (int)e;
+      if (!addr) return QMI_E_NULL_POINTER;
+      p = static_cast<float*>(addr);
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return QMI_OK;
+}
+
+}  // namespace
+
+extern "C" int qmi_paged_decode_attention_noalloc(
+    const uint16_t* q, int64_t q_seq_stride, int64_t q_head_stride, const uint16_t* k_cache,
+    const uint16_t* v_cache, int64_t num_blocks, int64_t block_size, int64_t num_q_heads,
+    int64_t num_kv_heads, int64_t head_dim, const int32_t* seqlens, int32_t seqlen_bias,
+    const int32_t* block_table, int64_t bt_stride, int64_t bt_width, int64_t batch, float scale,
+    uint16_t* out, int64_t out_seq_stride, int64_t out_head_stride, int64_t pages_per_split,
+    void* stream) {
+  // Shapes the regular entry point rejects are rejected the same way, before
+  // any HIP call: it is handed a null workspace of size 0 only when nothing
+  // is launched (batch 0) or an argument is invalid.
+  if (batch < 0 || num_blocks < 0 || bt_width < 0) return QMI_E_BAD_SHAPE;
+  if (batch == 0) return QMI_OK;
+  if (num_blocks == 0 || bt_width == 0) return QMI_E_BAD_SHAPE;
+  if (!q || !k_cache || !v_cache || !seqlens || !block_table || !out) return QMI_E_NULL_POINTER;
+  if (head_dim != kHeadDim || block_size != kPage) return QMI_E_UNSUPPORTED;
+  if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads != 0)
+    return QMI_E_BAD_SHAPE;
+  const int64_t need =
+      qmi_paged_decode_workspace_bytes(batch, num_kv_heads, num_q_heads, bt_width, pages_per_split);
+  if (need > kDecodeScratchBytes) return QMI_E_SCRATCH_LIMIT;
+  float* ws = nullptr;
+  const int st = decode_scratch(&ws);
+  if (st != QMI_OK) return st;
+  return qmi_paged_decode_attention(q, q_seq_stride, q_head_stride, k_cache, v_cache, num_blocks,
+                                    block_size, num_q_heads, num_kv_heads, head_dim, seqlens,
+                                    seqlen_bias, block_table, bt_stride, bt_width, batch, scale,
+                                    out, out_seq_stride, out_head_stride, ws, kDecodeScratchBytes,
+                                    pages_per_split, stream);
 }

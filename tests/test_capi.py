@@ -62,6 +62,17 @@ def test_validation_rejects_before_launch(pkg):
     st = L.qmi_paged_decode_attention(fake, 2048, 128, fake, fake, 16, 256, 16, 8, 128, fake, 1,
                                       fake, 4, 4, 4, 0.1, fake, 2048, 128, None, 0, 1, None)
     assert st == -5
+    # the no-allocation variant validates the same way before any HIP call
+    assert L.qmi_paged_decode_attention_noalloc(fake, 2048, 128, fake, fake, 16, 256, 16, 8, 128,
+                                                fake, 1, fake, 4, 4, 0, 0.1, fake, 2048, 128, 0,
+                                                None) == 0
+    assert L.qmi_paged_decode_attention_noalloc(None, 2048, 128, fake, fake, 16, 256, 16, 8, 128,
+                                                fake, 1, fake, 4, 4, 4, 0.1, fake, 2048, 128, 0,
+                                                None) == -1
+    assert L.qmi_paged_decode_attention_noalloc(fake, 2048, 128, fake, fake, 16, 128, 16, 8, 128,
+                                                fake, 1, fake, 4, 4, 4, 0.1, fake, 2048, 128, 0,
+                                                None) == -4
+    assert b"scratch" in L.qmi_error_string(-6)
     assert 0 < L.qmi_grpo_fused_workspace_bytes(32, 512) < 4096
     assert L.qmi_ppo_clipped_loss(None, None, None, None, 1, 0, 2, 3, 0.2, 0, None, None, None) == -1
     assert L.qmi_ppo_clipped_loss(fake, fake, fake, fake, 1, 0, 2, 3, 0.2, 7, fake, None, None) == -4
