@@ -462,8 +462,16 @@ extern "C" int qmi_paged_decode_attention_noalloc(
   if (head_dim != kHeadDim || block_size != kPage) return QMI_E_UNSUPPORTED;
   if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads != 0)
     return QMI_E_BAD_SHAPE;
+  // The workspace the call will use: the balanced schedule's when it takes
+  // that path (the regular entry point's condition), else the per-split one's.
+  const bool balanced = pages_per_split <= 0 &&
+                        qmi::streamk_supported(num_q_heads, num_kv_heads, batch) &&
+                        aligned16(out) && out_seq_stride % 8 == 0 && out_head_stride % 8 == 0;
+  const int64_t pps = pages_per_split > 0 ? pages_per_split
+                                          : auto_pages_per_split(batch, num_kv_heads, bt_width);
   const int64_t need =
-      qmi_paged_decode_workspace_bytes(batch, num_kv_heads, num_q_heads, bt_width, pages_per_split);
+      balanced ? qmi::streamk_workspace_bytes(batch, num_q_heads, num_kv_heads, bt_width)
+               : qmi_paged_decode_workspace_bytes(batch, num_kv_heads, num_q_heads, bt_width, pps);
   if (need > kDecodeScratchBytes) return QMI_E_SCRATCH_LIMIT;
   float* ws = nullptr;
   const int st = decode_scratch(&ws);

@@ -71,3 +71,20 @@ def test_noalloc_rejects_problems_beyond_the_scratch(pkg, gpu):
     assert L.qmi_paged_decode_attention_noalloc(*_args(w2, out), 0,
                                                 torch.cuda.current_stream().cuda_stream) == SCRATCH_LIMIT
     assert b"static device scratch" in L.qmi_error_string(SCRATCH_LIMIT)
+
+
+def test_noalloc_balanced_schedule_with_graph_width_tables(pkg, gpu):
+    """256 sequences with page tables padded to 160 entries (the engine's
+    graph width): the balanced schedule needs 8.7 MB, within the array, even
+    though the per-split schedule of the same shape would need 34.6 MB."""
+    L = pkg._lib.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    w = W.decode_batch(seed=7, device=gpu, batch=256, ctx_lo=100, ctx_hi=1100)
+    bt = torch.full((256, 160), -1, dtype=torch.int32, device=gpu)
+    bt[:, :w["block_tables"].shape[1]] = w["block_tables"]
+    w = dict(w, block_tables=bt)
+    print("[noalloc] B=256, table width 160", flush=True)
+    ref = _regular(L, w, 0, stream)
+    got = _noalloc(L, w, 0, stream)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
