@@ -147,6 +147,131 @@ def leg_decode(torch, pkg, W, dev, steps, warmup, layers=28):
                 workload=w)
 
 
+def init_qwen3_weights(torch, model, std=0.02):
+    """Random init as transformers initialises Qwen3: N(0, std) matrices and
+    embedding (tied lm_head), unit norm weights."""
+    with torch.no_grad():
+        for name, p in model.named_parameters():
+            if "norm" in name:
+                p.fill_(1.0)
+            else:
+                p.normal_(0.0, std)
+
+
+def make_qwen3(torch, pkg, dev, seed=0):
+    torch.manual_seed(seed)
+    with torch.device(dev):
+        model = pkg.Qwen3ForCausalLM(pkg.Qwen3Config())
+    init_qwen3_weights(torch, model)
+    return model.to(torch.bfloat16).eval()
+
+
+def leg_decode_step(torch, pkg, dev, steps, warmup, w, attn_ms_step):
+    """Config 3 as a whole: one 28-layer Qwen3-0.6B decode step for the
+    64-sequence serving batch (embedding, per layer add+RMSNorm, qkv GEMM,
+    fused QK-norm/RoPE/KV store, paged attention, o GEMM, add+RMSNorm,
+    gate_up GEMM, SwiGLU, down GEMM; final norm), captured as the engine's
+    HIP graph and replayed; then the lm_head and the fused sampler.  Uses the
+    decode leg's 28-layer pools, contexts and page tables (``w``)."""
+    log("decode_step: 28-layer model on the decode leg's pools")
+    model = make_qwen3(torch, pkg, dev)
+    for i, layer in enumerate(model.model.layers):
+        layer.self_attn.k_cache = w["k_cache"][i]
+        layer.self_attn.v_cache = w["v_cache"][i]
+    model._num_blocks = w["num_blocks"]
+    ctx, bt = w["context_lens"], w["block_tables"]
+    bsz = ctx.shape[0]
+    g = torch.Generator().manual_seed(1)
+    ids = torch.randint(0, 151936, (bsz,), generator=g).to(dev)
+    pos = ctx.long()
+    slots = (bt.long().gather(1, (pos // 256)[:, None])[:, 0] * 256 + pos % 256).to(torch.int32)
+    with torch.no_grad():
+        model._init_cuda_graphs(max_bs=bsz, bt_width=bt.shape[1])
+        model._capture_decode_graphs(batch_sizes=(bsz,))
+        assert model._has_cuda_graphs, "decode graph capture failed"
+        bufs = model._graph_bufs
+        bufs["input_ids"][:bsz] = ids
+        bufs["positions"][:bsz] = pos
+        bufs["slot_mapping"][:bsz] = slots
+        bufs["context_lens"][:bsz] = ctx
+        bufs["block_tables"][:bsz] = bt
+        graph = model._graphs[bsz]
+        h = bufs["outputs"][:bsz]
+        body_ms, _ = timed_launches(torch, [graph.replay], steps, warmup)
+        body_ms /= steps
+
+        def head():
+            return model._sample(model.lm_head(h), 1.0, None, True)
+        full_ms, _ = timed_launches(torch, [lambda: (graph.replay(), head())], steps, warmup)
+        full_ms /= steps
+        lm_ms, _ = timed_launches(torch, [lambda: model.lm_head(h)], steps, warmup)
+        lm_ms /= steps
+    weights = sum(p.numel() * 2 for p in model.parameters())
+    kv = W_kv_bytes(w)
+    out = dict(ms_per_step=body_ms, ms_per_step_with_lm_head_and_sampling=full_ms,
+               lm_head_ms=lm_ms, attention_ms_per_step=attn_ms_step,
+               attention_share=attn_ms_step / body_ms, batch=bsz,
+               weight_bytes=weights, kv_bytes_per_step=kv,
+               hbm_gbs=(kv + weights) / (body_ms * 1e-3) / 1e9)
+    model._graphs, model._graphs_units, model._graph_bufs, model._graph_pool = {}, {}, None, None
+    for layer in model.model.layers:
+        layer.self_attn.k_cache = layer.self_attn.v_cache = None
+    del model, graph, h
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return out
+
+
+def W_kv_bytes(w) -> int:
+    """K/V bytes a 28-layer decode step reads (ctx + 1 keys per sequence and layer)."""
+    return int(w["k_cache"].shape[0]) * int(w["kv_bytes"])
+
+
+def leg_lm_head(torch, pkg, dev, steps, warmup, vocab=151936, hidden=1024):
+    """Fused lm_head + sampling (rollout decode rows) and fused lm_head +
+    log-prob gather (loss-step rows) against the unfused pair they replace
+    (hipBLASLt logits GEMM, then the streaming sampler / log-prob kernel)."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    w = (0.02 * torch.randn((vocab, hidden), generator=g, device=dev)).to(torch.bfloat16)
+    out = {}
+    wbytes = vocab * hidden * 2
+    for n in (64, 256):
+        h = torch.randn((n, hidden), generator=g, device=dev).to(torch.bfloat16)
+        fused = lambda: pkg.kernels.lm_head_sample(h, w, 1.0, seed=1, offset=2)
+        unfused = lambda: pkg.kernels.sample_tokens(h @ w.T, 1.0, seed=1, offset=2)
+        gemm = lambda: h @ w.T
+        rec = {}
+        for name, fn in (("fused_us", fused), ("unfused_us", unfused), ("gemm_only_us", gemm)):
+            _, per = timed_launches(torch, [fn], steps, warmup)
+            rec[name] = round(statistics.median(per) * 1e3, 2)
+        flops = 2 * n * hidden * vocab
+        t = rec["fused_us"] * 1e-6
+        rec.update(rows=n, weight_bytes=wbytes, hbm_gbs=round(wbytes / t / 1e9, 1),
+                   frac_of_hbm_peak=round(wbytes / t / 1e9 / HBM_PEAK_GBS, 4),
+                   tflops=round(flops / t / 1e12, 1),
+                   frac_of_bf16_mfma_peak=round(flops / t / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4))
+        out[f"sample_{n}_rows"] = rec
+    n = 8192
+    h = torch.randn((n, hidden), generator=g, device=dev).to(torch.bfloat16)
+    tgt = torch.randint(0, vocab, (n,), generator=g, device=dev)
+    fused = lambda: pkg.kernels.lm_head_logprob(h, w, tgt)
+    unfused = lambda: pkg.kernels.logprob_gather(h @ w.T, tgt)
+    rec = {}
+    for name, fn in (("fused_us", fused), ("unfused_us", unfused)):
+        _, per = timed_launches(torch, [fn], max(3, steps // 4), warmup)
+        rec[name] = round(statistics.median(per) * 1e3, 1)
+    flops = 2 * n * hidden * vocab
+    rec.update(rows=n, tflops=round(flops / (rec["fused_us"] * 1e-6) / 1e12, 1),
+               frac_of_bf16_mfma_peak=round(flops / (rec["fused_us"] * 1e-6) / 1e12 /
+                                            MFMA_BF16_PEAK_TFLOPS, 4),
+               logits_bytes_not_materialised=n * vocab * 2)
+    out[f"logprob_{n}_rows"] = rec
+    del w, h
+    torch.cuda.empty_cache()
+    return out
+
+
 def leg_grpo(torch, pkg, W, dev, steps, warmup):
     log("grpo: generating 32x512x151936 bf16 logits")
     w = W.grpo_loss_step(seed=0, device=dev)
@@ -424,19 +549,22 @@ def leg_prefill(torch, pkg, W, dev, steps, warmup, cpu=True):
 
 # ---------------------------------------------------------------------------
 # End-to-end GRPO rollout + loss (config 5) and the reference-path baseline.
-class ReferencePath:
-    """Runs the engine the way the reference's non-kernel path would on this
-    GPU: torch ops for RMSNorm / RoPE / SwiGLU / KV store, attention as torch
-    SDPA over K/V gathered through the block table (flash-attn is not in this
-    image), eager decode without graphs.  Bench-only: the product has one
-    backend."""
+class TorchBody:
+    """Model body of the torch reference path: torch ops for RMSNorm, QK-norm,
+    RoPE, SwiGLU and the KV store (index_copy_), and attention as torch SDPA
+    over K/V gathered for the keys each sequence needs (decode: padded to the
+    step's longest context, the two query heads of a KV head folded into the
+    query length, so no K/V copy per query head; prefill: per sequence).
+    flash-attn is not installed in this image.  Bench-only: the product has
+    one backend."""
+
+    attention_kind = "torch SDPA (memory-efficient / flash backends, bf16)"
 
     def __init__(self, torch, pkg):
         self.torch, self.pkg = torch, pkg
         self.QN = pkg.qwen3_naive
 
     def _project(self, attn, x, positions):
-        t = self.torch
         qkv = attn.qkv_proj(x)
         n = x.shape[0]
         q, k, v = qkv.split([attn.q_size, attn.kv_size, attn.kv_size], dim=-1)
@@ -444,26 +572,24 @@ class ReferencePath:
         k = attn.k_norm(k.reshape(n, attn.num_kv_heads, attn.head_dim))
         cache = attn._cos_sin(x.device)
         rot = self.QN.RotaryEmbedding.rotate
-        return rot(q, positions, cache), rot(k, positions, cache), v.reshape(n, attn.num_kv_heads, attn.head_dim)
+        return (rot(q, positions, cache), rot(k, positions, cache),
+                v.reshape(n, attn.num_kv_heads, attn.head_dim))
 
     def _store(self, attn, k, v, slots):
-        # Eager steps carry no -1 (padding) slots, so a plain index_copy_ is exact.
         row = attn.num_kv_heads * attn.head_dim
         idx = slots.long()
         attn.k_cache.view(-1, row).index_copy_(0, idx, k.reshape(-1, row))
         attn.v_cache.view(-1, row).index_copy_(0, idx, v.reshape(-1, row))
 
-    attention_kind = "torch SDPA (memory-efficient backend, bf16)"
-
     def _sdpa(self, q, k, v, mask):
         t = self.torch
         from torch.nn.attention import SDPBackend, sdpa_kernel
-        if ReferencePath.attention_kind.startswith("torch SDPA"):
+        if TorchBody.attention_kind.startswith("torch SDPA"):
             try:
                 with sdpa_kernel([SDPBackend.EFFICIENT_ATTENTION, SDPBackend.FLASH_ATTENTION]):
                     return t.nn.functional.scaled_dot_product_attention(q, k, v, attn_mask=mask)
             except RuntimeError:
-                ReferencePath.attention_kind = "fp32 matmul attention (no fused SDPA kernel)"
+                TorchBody.attention_kind = "fp32 matmul attention (no fused SDPA kernel)"
         # fp32 products: batched bf16 products with transposed operands are
         # avoided on this platform.
         s = t.matmul(q.float(), k.float().transpose(-2, -1).contiguous()) * q.shape[-1] ** -0.5
@@ -474,15 +600,18 @@ class ReferencePath:
         t = self.torch
         q, k, v = self._project(attn, x, positions)
         self._store(attn, k, v, slot_mapping)
-        bsz, w = block_tables.shape
-        bt = block_tables.clamp(min=0).long()
-        kk = attn.k_cache[bt].reshape(bsz, w * 256, attn.num_kv_heads, attn.head_dim)
-        vv = attn.v_cache[bt].reshape(bsz, w * 256, attn.num_kv_heads, attn.head_dim)
-        rep = attn.num_heads // attn.num_kv_heads
-        kk = kk.transpose(1, 2).repeat_interleave(rep, 1)
-        vv = vv.transpose(1, 2).repeat_interleave(rep, 1)
-        mask = (t.arange(w * 256, device=x.device)[None, :] <= context_lens.long()[:, None])
-        o = self._sdpa(q[:, :, None, :], kk, vv, mask[:, None, None, :])
+        bsz = x.shape[0]
+        lens = context_lens.long() + 1
+        lmax = int(lens.max())
+        npg = -(-lmax // 256)
+        bt = block_tables[:, :npg].clamp(min=0).long()
+        hkv, d = attn.num_kv_heads, attn.head_dim
+        rep = attn.num_heads // hkv
+        kk = attn.k_cache[bt].reshape(bsz, npg * 256, hkv, d)[:, :lmax].transpose(1, 2)
+        vv = attn.v_cache[bt].reshape(bsz, npg * 256, hkv, d)[:, :lmax].transpose(1, 2)
+        mask = (t.arange(lmax, device=x.device)[None, :] < lens[:, None])[:, None, None, :]
+        qg = q.view(bsz, hkv, rep, d)              # query head h -> KV head h // rep
+        o = self._sdpa(qg, kk, vv, mask)
         return attn.o_proj(o.reshape(bsz, -1))
 
     def prefill(self, attn, x, positions, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
@@ -523,14 +652,139 @@ class ReferencePath:
         return False
 
 
+class ReferenceEngine:
+    """The reference's rollout loop, generate_continuous_with_logprobs
+    (qwen3_naive.py:1474-1679), restated over this model as the end-to-end
+    baseline.  Kept from the reference:
+      * the scheduler: decode first, LIFO preemption, 2,048-token budget
+        (:1499-1585; the model's own _schedule, which follows it);
+      * decode as HIP graphs only for batches of at most 64 (buckets
+        1, 2, 4, 8, 16, 32, 48, 64, page-table width min(pool, 160),
+        :1070-1145), eager above;
+      * lm_head over every token of the step (:1607), then the sampled rows;
+      * sampling with torch ops: fp32 logits / T, optional top-k mask,
+        softmax, multinomial, log_softmax + gather (:1632-1650), and two
+        .item() reads per sampled sequence (:1656-1659);
+      * no decode lookahead.
+    ``body``: "torch" runs TorchBody (eager at every batch size: a torch
+    attention over varying lengths cannot be captured); "kernels" keeps this
+    build's HIP kernels as stand-ins for the reference's flash-attn / Triton /
+    inductor kernels (one fused kernel each there too), so only the engine
+    structure differs from the product.  Bench-only."""
+
+    GRAPH_BS = (1, 2, 4, 8, 16, 32, 48, 64)
+
+    def __init__(self, torch, pkg, model, body):
+        self.torch, self.pkg, self.m, self.body = torch, pkg, model, body
+        self.stats = {}
+
+    def _swap_graph_state(self, state=None):
+        m = self.m
+        keys = ("_graphs", "_graphs_units", "_graph_bufs", "_graph_pool", "_graph_in",
+                "_graph_max_bs", "_has_cuda_graphs")
+        old = {k: getattr(m, k, None) for k in keys}
+        if state is not None:
+            for k, v in state.items():
+                setattr(m, k, v)
+        return old
+
+    def setup(self):
+        """Capture the reference's decode graphs (kernels body), outside any timing."""
+        if self.body != "kernels":
+            return
+        m = self.m
+        saved = self._swap_graph_state()
+        with self.torch.no_grad():
+            m._init_cuda_graphs(max_bs=64, bt_width=min(m._num_blocks, 160))
+            m._capture_decode_graphs(batch_sizes=self.GRAPH_BS)
+        self._ref_state = self._swap_graph_state(saved)
+
+    def generate(self, prompts, max_new_tokens, temperature=1.0, top_k=None):
+        t, m, P = self.torch, self.m, self.pkg.paged
+        from collections import deque
+        bm = P.BlockManager(m._num_blocks, m.BLOCK_SIZE)
+        waiting = deque(P.Sequence(p[0].tolist(), {"temperature": temperature,
+                                                   "max_tokens": max_new_tokens})
+                        for p in prompts)
+        all_seqs = list(waiting)
+        running = []
+        m._preemptions = 0
+        st = {"steps": 0, "decode_steps": 0, "graph_steps": 0, "item_reads": 0}
+        ctx = TorchBody(t, self.pkg) if self.body == "torch" else None
+        saved = self._swap_graph_state(getattr(self, "_ref_state", None)) if self.body == "kernels" else None
+        try:
+            if ctx is not None:
+                ctx.__enter__()
+            with t.no_grad():
+                while waiting or running:
+                    sched = m._schedule(waiting, running, bm)
+                    if not sched:
+                        continue
+                    st["steps"] += 1
+                    all_decode = all(s.num_scheduled_tokens == 1 for s in sched)
+                    if all_decode:
+                        st["decode_steps"] += 1
+                        ids, pos, cl, bt, slots = m._prepare_decode(sched)
+                        h = None
+                        if self.body == "kernels" and len(sched) <= 64:
+                            h = m._run_decode_graph(len(sched), ids, pos, cl, bt, slots)
+                            st["graph_steps"] += h is not None
+                        if h is None:
+                            h = m.model.forward_decode(ids, pos, cl, bt, slots)
+                    else:
+                        ids, pos, cu_q, cu_k, mq, mk, bmap, bt = m._prepare_step(sched)
+                        h = m.model.forward_prefill(ids, pos, cu_q, cu_k, mq, mk, bmap, bt)
+                    logits = m.lm_head(h)
+                    for s in sched:
+                        s.kv_len += s.num_scheduled_tokens
+                        if not all_decode:
+                            bm.hash_blocks(s)
+                    idx, off = [], 0
+                    for s in sched:
+                        if s.num_scheduled_tokens == 1 or s.kv_len >= s.num_prompt_tokens:
+                            idx.append(off + s.num_scheduled_tokens - 1)
+                        off += s.num_scheduled_tokens
+                    if not idx:
+                        for s in sched:
+                            s.num_scheduled_tokens = 0
+                        continue
+                    last = logits[idx].float() / temperature
+                    if top_k is not None:
+                        vals, tix = t.topk(last, top_k, dim=-1)
+                        last = t.full_like(last, float("-inf")).scatter(-1, tix, vals)
+                    probs = t.softmax(last, dim=-1)
+                    nxt = t.multinomial(probs, num_samples=1)
+                    slp = t.log_softmax(last, dim=-1).gather(-1, nxt)
+                    j = 0
+                    for s in sched:
+                        if s.num_scheduled_tokens == 1 or s.kv_len >= s.num_prompt_tokens:
+                            tok = nxt[j].item()
+                            s.append_token(tok)
+                            s.response_log_probs.append(slp[j].item())
+                            st["item_reads"] += 2
+                            j += 1
+                            if s.num_completion_tokens >= s.max_tokens:
+                                s.status = "FINISHED"
+                                bm.deallocate(s.block_table)
+                                s.block_table.clear()
+                                running.remove(s)
+                        s.num_scheduled_tokens = 0
+        finally:
+            if ctx is not None:
+                ctx.__exit__(None, None, None)
+            if saved is not None:
+                self._ref_state = self._swap_graph_state(saved)
+        st["preemptions"] = m._preemptions
+        self.stats = st
+        return ([s.token_ids for s in all_seqs], [s.token_ids[s.num_prompt_tokens:] for s in all_seqs],
+                [list(s.response_log_probs) for s in all_seqs], [s.num_prompt_tokens for s in all_seqs])
+
+
 def make_rollout_model(torch, pkg, dev, pool_gb=40.0):
-    """Random-init Qwen3-0.6B (28 layers, tied lm_head) in bf16 with a KV pool of
-    ``pool_gb`` GB (40 GB -> 1,362 blocks of 29.36 MB)."""
-    torch.manual_seed(0)
-    cfg = pkg.Qwen3Config()
-    with torch.device(dev):
-        model = pkg.Qwen3ForCausalLM(cfg)
-    model = model.to(torch.bfloat16).eval()
+    """Random-init Qwen3-0.6B (28 layers, tied lm_head, transformers' N(0, 0.02)
+    initialisation) in bf16 with a KV pool of ``pool_gb`` GB (40 GB -> 1,362
+    blocks of 29.36 MB)."""
+    model = make_qwen3(torch, pkg, dev)
     model.allocate_global_kv_cache(num_blocks=int(pool_gb * 1e9 // model.kv_block_bytes()))
     return model
 
@@ -542,9 +796,11 @@ def rollout_prompts(torch, n_prompts=32, group=8, prompt_len=128, vocab=151936, 
 
 
 def grpo_loss_after_rollout(torch, pkg, model, seqs, plens, lps, n_prompts, group, micro=16, seed=0):
-    """New log-probs of every generated token (prefill forward, micro-batched),
-    seeded Bernoulli(0.5) rewards, group advantages and the clipped loss
-    (per-sequence masked mean), next-token alignment."""
+    """New log-probs of every generated token (prefill forward to the final
+    hidden states, then the fused lm_head + log-prob kernel: no logits are
+    materialised), seeded Bernoulli(0.5) rewards, group advantages and the
+    clipped loss (per-sequence masked mean), next-token alignment;
+    micro-batched over sequences."""
     dev = next(model.parameters()).device
     g = torch.Generator().manual_seed(seed)
     rewards = torch.bernoulli(torch.full((len(seqs),), 0.5), generator=g).to(dev)
@@ -564,67 +820,97 @@ def grpo_loss_after_rollout(torch, pkg, model, seqs, plens, lps, n_prompts, grou
                 objs.append(sq)
             ids, pos, cu_q, cu_k, mq, mk, bmap, bt = model._prepare_step(objs)
             h = model.model.forward_prefill(ids, pos, cu_q, cu_k, mq, mk, bmap, bt)
-            logits = model.lm_head(h).view(len(chunk), T, -1)
             ids2 = ids.view(len(chunk), T)
             old = torch.zeros((len(chunk), T), dtype=torch.float32, device=dev)
             mask = torch.zeros_like(old)
             for i, (pl, lp) in enumerate(zip(plens[s0:s0 + micro], lps[s0:s0 + micro])):
                 old[i, pl:pl + len(lp)] = torch.tensor(lp, device=dev)
                 mask[i, pl:pl + len(lp)] = 1.0
-            loss, _, _ = pkg.grpo_fused_loss(logits, ids2, old, mask, rewards[s0:s0 + micro],
-                                             pids[s0:s0 + micro], 1e-4, 0.2, "seq", shift=True)
+            loss, _, _ = pkg.grpo_loss_from_hidden(h.view(len(chunk), T, -1), model.lm_head.weight,
+                                                   ids2, old, mask, rewards[s0:s0 + micro],
+                                                   pids[s0:s0 + micro], 1e-4, 0.2, "seq",
+                                                   shift=True)
             total += loss.item() * len(chunk) / n_seq
-            del logits, h
+            del h
     return total
 
 
-def leg_rollout(torch, pkg, dev, new_tokens=1024, compare_tokens=64):
+def _timed(torch, fn):
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    out = fn()
+    torch.cuda.synchronize()
+    return out, time.perf_counter() - t0
+
+
+def leg_rollout(torch, pkg, dev, new_tokens=1024, compare_tokens=64, preempt_blocks=1200,
+                engines=("ours", "kernels", "torch")):
     """Config 5: 32 prompts x group 8 = 256 sequences, 128-token prompts, T=1.0,
     no top-k, ``new_tokens`` generated tokens each, continuous batching with the
-    2048-token step budget and LIFO preemption, ~40 GB pool; then the GRPO
-    loss over the generated tokens.  Also times ours and the reference path at
-    ``compare_tokens`` new tokens on the same workload."""
+    2048-token step budget and LIFO preemption, ~40 GB pool (1,362 blocks: no
+    preemption); then the GRPO loss over the generated tokens.  Also: the same
+    rollout in a ``preempt_blocks`` pool (under the 1,280 blocks 256 x 5 pages
+    need, so LIFO preemption fires), and ours against the reference engine's
+    loop (ReferenceEngine, two model bodies) at ``compare_tokens`` new tokens."""
     model = make_rollout_model(torch, pkg, dev)
     prompts = rollout_prompts(torch)
     n_tok = len(prompts)
+    gen = lambda n, **k: model.generate_continuous_with_logprobs(
+        prompts, max_new_tokens=n, temperature=1.0, top_k=None, **k)
     log("rollout: warm-up / graph capture")
     model.generate_continuous_with_logprobs(prompts[:16], max_new_tokens=4, temperature=1.0,
                                             top_k=None)
     out = {}
-    # Short comparison against the reference path (same scheduler, torch attention).
-    for name in (("ours_short", "reference_path_short") if compare_tokens > 0 else ()):
-        torch.manual_seed(1)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        if name == "ours_short":
-            model.generate_continuous_with_logprobs(prompts, max_new_tokens=compare_tokens,
-                                                    temperature=1.0, top_k=None)
-        else:
-            with ReferencePath(torch, pkg):
-                model.generate_continuous_with_logprobs(prompts, max_new_tokens=compare_tokens,
-                                                        temperature=1.0, top_k=None,
-                                                        use_graphs=False)
-        torch.cuda.synchronize()
-        out[name] = n_tok * compare_tokens / (time.perf_counter() - t0)
-        log(f"rollout: {name} {out[name]:.0f} tok/s")
+    if compare_tokens > 0:
+        if "ours" in engines:
+            torch.manual_seed(1)
+            _, dt = _timed(torch, lambda: gen(compare_tokens))
+            out["ours_short"] = dict(tokens_per_s=n_tok * compare_tokens / dt, s=dt,
+                                     **dict(model.last_stats))
+            log(f"rollout: ours {out['ours_short']['tokens_per_s']:.0f} tok/s at "
+                f"{compare_tokens} tokens")
+        for body in [e for e in ("kernels", "torch") if e in engines]:
+            ref = ReferenceEngine(torch, pkg, model, body)
+            ref.setup()
+            torch.manual_seed(1)
+            _, dt = _timed(torch, lambda: ref.generate(prompts, compare_tokens, 1.0, None))
+            out[f"reference_{body}_short"] = dict(tokens_per_s=n_tok * compare_tokens / dt, s=dt,
+                                                  **ref.stats)
+            log(f"rollout: reference engine ({body} body) "
+                f"{out[f'reference_{body}_short']['tokens_per_s']:.0f} tok/s")
+            del ref
+        torch.cuda.empty_cache()
+    if new_tokens <= 0:
+        del model
+        torch.cuda.empty_cache()
+        return out
     log(f"rollout: full run ({n_tok} x {new_tokens} tokens)")
     torch.manual_seed(2)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    toks, gen, lps, plens = model.generate_continuous_with_logprobs(
-        prompts, max_new_tokens=new_tokens, temperature=1.0, top_k=None)
-    torch.cuda.synchronize()
-    t_roll = time.perf_counter() - t0
+    (toks, gen_t, lps, plens), t_roll = _timed(torch, lambda: gen(new_tokens))
     stats = dict(model.last_stats)
     t0 = time.perf_counter()
     loss = grpo_loss_after_rollout(torch, pkg, model, toks, plens, lps, 32, 8)
     torch.cuda.synchronize()
     t_loss = time.perf_counter() - t0
-    generated = sum(len(x) for x in gen)
+    generated = sum(len(x) for x in gen_t)
     assert len(set(len(x) for x in toks)) == 1, "fixed-length rollout expected (no EOS)"
     out.update(dict(generated=generated, rollout_s=t_roll, loss_s=t_loss, loss=loss,
                     tokens_per_s=generated / t_roll, tokens_per_s_with_loss=generated / (t_roll + t_loss),
                     num_blocks=model._num_blocks, **stats))
+    del toks, gen_t, lps
+    if preempt_blocks:
+        log(f"rollout: {preempt_blocks}-block pool (forced LIFO preemption)")
+        model.allocate_global_kv_cache(num_blocks=preempt_blocks)
+        model.generate_continuous_with_logprobs(prompts[:16], max_new_tokens=4, temperature=1.0,
+                                                top_k=None)
+        torch.manual_seed(2)
+        (_, gen_p, _, _), dt = _timed(torch, lambda: gen(new_tokens))
+        gen_n = sum(len(x) for x in gen_p)
+        assert gen_n == generated
+        out["preempt"] = dict(num_blocks=preempt_blocks, rollout_s=dt, tokens_per_s=gen_n / dt,
+                              **dict(model.last_stats))
+        log(f"rollout: preemption run {gen_n / dt:.0f} tok/s, "
+            f"{model.last_stats['preemptions']} preemptions")
     del model
     torch.cuda.empty_cache()
     return out
@@ -766,11 +1052,17 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--legs", default="decode1,decode,grpo,store,prefill,norm_rope,host,rollout")
+    ap.add_argument("--legs",
+                    default="decode1,decode,decode_step,lm_head,grpo,store,prefill,norm_rope,host,rollout")
     ap.add_argument("--rollout-tokens", type=int, default=1024,
                     help="new tokens per sequence in the end-to-end rollout leg")
     ap.add_argument("--rollout-compare-tokens", type=int, default=64,
-                    help="new tokens of the short ours-vs-reference-path comparison (0 skips it)")
+                    help="new tokens of the short ours-vs-reference-engine comparison (0 skips it)")
+    ap.add_argument("--rollout-engines", default="ours,kernels,torch",
+                    help="engines of that comparison: ours, kernels (reference loop, this "
+                         "build's kernels), torch (reference loop, torch body)")
+    ap.add_argument("--rollout-preempt-blocks", type=int, default=1200,
+                    help="pool of the forced-preemption rollout (0 skips it)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 1 GiB device copy (counter calibration)")
@@ -806,8 +1098,14 @@ def main() -> int:
             log("cpu baseline (oracle decode)")
             cpu = cpu_baseline_decode(torch, W, results["decode"]["workload"])
         results["decode"]["kv_pool_gb"] = results["decode"]["workload"]["k_cache"].numel() * 4 / 1e9
+        if "decode_step" in legs:
+            results["decode_step"] = leg_decode_step(torch, pkg, dev, max(5, args.steps // 2),
+                                                     args.warmup, results["decode"]["workload"],
+                                                     results["decode"]["ms_per_step"])
         del results["decode"]["workload"]
         torch.cuda.empty_cache()
+    if "lm_head" in legs:
+        results["lm_head"] = leg_lm_head(torch, pkg, dev, args.steps, args.warmup)
     if "grpo" in legs:
         results["grpo"] = leg_grpo(torch, pkg, W, dev, max(3, args.steps // 2), args.warmup)
     if "store" in legs:
@@ -821,7 +1119,9 @@ def main() -> int:
         results["host"] = leg_host_prepare(torch, pkg)
     if "rollout" in legs:
         results["rollout"] = leg_rollout(torch, pkg, dev, new_tokens=args.rollout_tokens,
-                                         compare_tokens=args.rollout_compare_tokens)
+                                         compare_tokens=args.rollout_compare_tokens,
+                                         preempt_blocks=args.rollout_preempt_blocks,
+                                         engines=tuple(args.rollout_engines.split(",")))
 
     cpu_grpo = None
     if not args.no_cpu and "grpo" in results:
@@ -864,6 +1164,32 @@ def main() -> int:
                         "K and V rows out); RMSNorm / add + RMSNorm / SwiGLU over 8,192 rows; "
                         "HIP graphs of 20 launches", **results["norm_rope"]}
 
+    if "lm_head" in results:
+        secondary["lm_head_fused"] = {
+            "workload": "fused lm_head (hidden 1024 x vocab 151936 bf16, fp32 logits never "
+                        "materialised) + inverse-CDF sampling with the drawn token's log-prob "
+                        "(sample_*), or + target log-prob gather (logprob_*); against the "
+                        "unfused hipBLASLt GEMM + streaming sampler / log-prob kernel",
+            **results["lm_head"]}
+
+    if "decode_step" in results:
+        r = results["decode_step"]
+        secondary["decode_step_28layer_b64"] = {
+            "workload": "one full Qwen3-0.6B decode step (28 layers, random-init bf16 weights) "
+                        "for 64 sequences, contexts U{1024..4096}, shuffled page tables, as the "
+                        "engine's HIP graph (embedding, norms, GEMMs, fused QK-norm/RoPE/KV "
+                        "store, paged attention, SwiGLU, final norm); lm_head + fused sampler "
+                        "timed after it",
+            "ms_per_step": round(r["ms_per_step"], 4),
+            "ms_per_step_with_lm_head_and_sampling":
+                round(r["ms_per_step_with_lm_head_and_sampling"], 4),
+            "lm_head_ms": round(r["lm_head_ms"], 4),
+            "attention_ms_per_step": round(r["attention_ms_per_step"], 4),
+            "attention_share": round(r["attention_share"], 4),
+            "kv_bytes_per_step": r["kv_bytes_per_step"], "weight_bytes": r["weight_bytes"],
+            "hbm_gbs_kv_plus_weights": round(r["hbm_gbs"], 1),
+            "frac_of_hbm_peak": round(r["hbm_gbs"] / HBM_PEAK_GBS, 4)}
+
     if "host" in results:
         secondary["host_decode_prepare"] = {
             "workload": "host-side decode step inputs (new-token slots, -1-padded page tables, "
@@ -894,7 +1220,7 @@ def main() -> int:
             if k in r:
                 secondary["prefill_attention"][k] = r[k]
 
-    if "rollout" in results:
+    if "rollout" in results and "tokens_per_s" in results["rollout"]:
         r = results["rollout"]
         secondary["grpo_rollout"] = {
             "workload": "random-init Qwen3-0.6B bf16, 32 prompts x group 8 = 256 seqs, 128-token "
@@ -908,14 +1234,38 @@ def main() -> int:
             "preemptions": r.get("preemptions"), "engine_steps": r.get("steps"),
             "graph_decode_steps": r.get("graph_steps"),
             "lookahead_decode_steps": r.get("lookahead_steps")}
+        if "preempt" in r:
+            pr = r["preempt"]
+            secondary["grpo_rollout"]["forced_preemption"] = {
+                "kv_blocks": pr["num_blocks"], "tokens_per_s": round(pr["tokens_per_s"], 1),
+                "rollout_s": round(pr["rollout_s"], 3), "preemptions": pr["preemptions"],
+                "engine_steps": pr["steps"], "graph_decode_steps": pr["graph_steps"],
+                "lookahead_decode_steps": pr["lookahead_steps"]}
         if "ours_short" in r:
-            secondary["grpo_rollout"][f"short_compare_{args.rollout_compare_tokens}_tokens"] = {
-                "ours_tokens_per_s": round(r["ours_short"], 1),
-                "reference_path_tokens_per_s": round(r["reference_path_short"], 1),
-                "reference_path": "same scheduler; torch RMSNorm/RoPE/SwiGLU/store; attention = "
-                                  f"{ReferencePath.attention_kind} over block-table-gathered K/V "
-                                  "(flash-attn unavailable); eager decode",
-                "speedup": round(r["ours_short"] / r["reference_path_short"], 2)}
+            o = r["ours_short"]
+            cmp = {"new_tokens": args.rollout_compare_tokens,
+                   "ours_tokens_per_s": round(o["tokens_per_s"], 1)}
+            for body, desc in (
+                    ("kernels", "the reference's engine loop (graphs only up to batch 64, "
+                                "lm_head over every token, torch softmax / multinomial / "
+                                "log_softmax with two .item() per sequence per step, no "
+                                "lookahead) with this build's kernels standing in for its "
+                                "flash-attn / Triton / inductor kernels"),
+                    ("torch", "the same loop with a torch body: torch norms / RoPE / SwiGLU / "
+                              f"store and {TorchBody.attention_kind} over the K/V each "
+                              "sequence needs, eager at every batch size (flash-attn is not "
+                              "installed)")):
+                rr = r.get(f"reference_{body}_short")
+                if rr is None:
+                    continue
+                cmp[f"reference_engine_{body}_body"] = {
+                    "description": desc, "tokens_per_s": round(rr["tokens_per_s"], 1),
+                    "engine_steps": rr["steps"], "decode_steps": rr["decode_steps"],
+                    "graph_decode_steps": rr["graph_steps"],
+                    "ms_per_step": round(rr["s"] / rr["steps"] * 1e3, 3),
+                    "speedup_of_ours": round(o["tokens_per_s"] / rr["tokens_per_s"], 2)}
+            cmp["ours_ms_per_step"] = round(o["s"] / o["steps"] * 1e3, 3)
+            secondary["grpo_rollout"]["reference_engine_comparison"] = cmp
 
     if "decode" in results:
         d = results["decode"]

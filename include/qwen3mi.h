@@ -114,10 +114,13 @@ int qmi_paged_decode_attention(const uint16_t* q, int64_t q_seq_stride, int64_t 
  * qmi_paged_decode_attention without the workspace pair; the kernels use a
  * 16 MiB static device array instead (one per device, held until the
  * process ends; its address is looked up on the first call on a device, so
- * make that first call outside a graph capture).  Problems whose
- * qmi_paged_decode_workspace_bytes() exceeds 16 MiB are rejected with
- * QMI_E_SCRATCH_LIMIT before anything is launched (Qwen3-0.6B's 16 / 8
- * heads need 8.7 MB on 256 CUs at any batch up to 1024).  The array keeps
+ * make that first call outside a graph capture).  Problems whose schedule
+ * needs more than 16 MiB of workspace are rejected with QMI_E_SCRATCH_LIMIT
+ * before anything is launched: the balanced schedule needs at most
+ * 2 x CUs x 2 x num_q_heads x 528 B + 4 (batch + 2) B (Qwen3-0.6B's 16 query
+ * heads: 8.7 MB on 256 CUs at any batch up to 1024); the per-split schedule
+ * (pages_per_split > 0, or layouts the balanced one does not take) needs
+ * batch x num_q_heads x splits x 528 B.  The array keeps
  * the last call's contents and needs no clearing, but calls that overlap on
  * one device share it and race: serialise them (one stream, or events).
  */
@@ -367,6 +370,45 @@ int qmi_logprob_gather_backward(const uint16_t* logits, int64_t logit_seq_stride
 int qmi_sample_tokens(const uint16_t* logits, int64_t row_stride, int64_t n_rows, int64_t vocab,
                       float temperature, uint64_t seed, uint64_t offset, int64_t* out_tokens,
                       float* out_logprobs, void* stream);
+
+/*
+ * Fused lm_head + sampling: logits = hidden_states . weight^T accumulated in
+ * fp32 and never materialised, then one token per row drawn from
+ * softmax(logits / temperature) with its log-probability.  Replaces
+ * `logits = self.lm_head(h)` (qwen3_naive.py:1387, :1607) and, for
+ * top_k = None, the sampling step of generate_continuous (:1413-1423) and
+ * generate_continuous_with_logprobs (:1636-1650).
+ * hidden_states: [n_rows, hidden] bf16 (row stride h_stride); weight:
+ * [vocab, hidden] bf16 (row stride w_stride); hidden a multiple of 64,
+ * pointers 16-byte aligned, strides multiples of 8.
+ * Draw: inverse transform sampling -- the first vocabulary index whose
+ * cumulative probability exceeds u, with u = (53 bits of words 0 and 1 of
+ * Philox4x32-10 at counter (0, row, offset_lo, offset_hi), key (seed_lo,
+ * seed_hi)) + 0.5, scaled by 2^-53.  A (seed, offset) pair reproduces the
+ * tokens.  out_tokens int64 [n_rows]; out_logprobs fp32 [n_rows] or NULL.
+ * workspace: qmi_lm_head_workspace_bytes(n_rows, vocab) bytes, 16-byte
+ * aligned (per-row, per-128-entry-tile softmax pairs; no initial contents).
+ */
+int64_t qmi_lm_head_workspace_bytes(int64_t n_rows, int64_t vocab);
+
+int qmi_lm_head_sample(const uint16_t* hidden_states, int64_t h_stride, int64_t n_rows,
+                       const uint16_t* weight, int64_t w_stride, int64_t vocab, int64_t hidden,
+                       float temperature, uint64_t seed, uint64_t offset, int64_t* out_tokens,
+                       float* out_logprobs, void* workspace, int64_t workspace_bytes,
+                       void* stream);
+
+/*
+ * Fused lm_head + log-softmax gather: out_logprobs[r] =
+ * log_softmax(hidden_states[r] . weight^T)[targets[r * target_stride]] and
+ * out_lse[r] (may be NULL) its log-sum-exp, the logits fp32 and never
+ * materialised.  Replaces `model(input_ids)`'s lm_head (qwen3_naive.py:826-835)
+ * plus forward_logprob's gather (qwen3_grpo_train.py:46-53) for the rows
+ * given.  Layout and workspace as qmi_lm_head_sample.
+ */
+int qmi_lm_head_logprob(const uint16_t* hidden_states, int64_t h_stride, int64_t n_rows,
+                        const uint16_t* weight, int64_t w_stride, int64_t vocab, int64_t hidden,
+                        const int64_t* targets, int64_t target_stride, float* out_logprobs,
+                        float* out_lse, void* workspace, int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

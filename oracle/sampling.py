@@ -71,3 +71,31 @@ def logprob_of(logits: torch.Tensor, tokens: torch.Tensor, temperature: float) -
     """log_softmax(logits.float() / T)[tok] (qwen3_naive.py:1646-1650), float64."""
     lp = torch.log_softmax(logits.double() / temperature, dim=-1)
     return lp.gather(-1, tokens.long().view(-1, 1))[:, 0]
+
+
+# ---------------------------------------------------------------------------
+# Inverse transform sampling with one uniform per row (the fused lm_head
+# sampler's draw).  Follows the same reference lines (top_k = None); the draw
+# is tok = min{i : sum_{j <= i} p_j > u}, an exact sample of Categorical(p).
+
+def uniform53(n_rows: int, seed: int, offset: int) -> np.ndarray:
+    """u[r] in (0, 1): words 0 and 1 of Philox4x32-10 at counter
+    (0, r, offset_lo, offset_hi), key (seed_lo, seed_hi), as
+    ((w0 << 21 | w1 >> 11) + 0.5) / 2^53 (float64)."""
+    ctr = np.zeros((n_rows, 4), dtype=np.uint32)
+    ctr[:, 1] = np.arange(n_rows, dtype=np.uint32)
+    ctr[:, 2] = offset & _MASK
+    ctr[:, 3] = (offset >> 32) & _MASK
+    w = philox4x32_10(ctr, (seed & _MASK, (seed >> 32) & _MASK))
+    bits = (w[:, 0].astype(np.uint64) << np.uint64(21)) | (w[:, 1].astype(np.uint64) >> np.uint64(11))
+    return (bits.astype(np.float64) + 0.5) / 2.0 ** 53
+
+
+def inverse_cdf_draw(logits: torch.Tensor, temperature: float, u: np.ndarray) -> np.ndarray:
+    """First index whose cumulative softmax(logits / T) probability exceeds
+    u (float64), per row."""
+    p = probs(logits, temperature).numpy()
+    cdf = np.cumsum(p, axis=-1)
+    idx = np.array([np.searchsorted(cdf[r], u[r], side="right") for r in range(p.shape[0])])
+    last = np.array([np.flatnonzero(p[r] > 0)[-1] for r in range(p.shape[0])])
+    return np.minimum(idx, last)

@@ -18,12 +18,12 @@ from .qwen3_naive import (  # noqa: F401
     RMSNorm, RotaryEmbedding, load_weights)
 from .qwen3_grpo_train import (  # noqa: F401
     compute_grpo_advantage, forward_logprob, grpo_fused_loss, grpo_fused_train_step,
-    grpo_train_step, ppo_clipped_loss)
+    grpo_loss_from_hidden, grpo_train_step, ppo_clipped_loss)
 
 __all__ = [
     "kernels", "paged", "qwen3_naive", "qwen3_grpo_train", "store_kvcache", "BlockManager",
     "Sequence", "Qwen3Attention", "Qwen3Config", "Qwen3DecoderLayer", "Qwen3ForCausalLM",
     "Qwen3MLP", "Qwen3Model", "RMSNorm", "RotaryEmbedding", "load_weights",
     "compute_grpo_advantage", "forward_logprob", "grpo_fused_loss", "grpo_fused_train_step",
-    "grpo_train_step", "ppo_clipped_loss",
+    "grpo_loss_from_hidden", "grpo_train_step", "ppo_clipped_loss",
 ]

@@ -32,18 +32,6 @@ using namespace qmi;
 constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / 64;
 
-__device__ __forceinline__ uint4 philox4x32_10(uint4 c, uint32_t k0, uint32_t k1) {
-#pragma unroll
-  for (int r = 0; r < 10; ++r) {
-    const uint32_t lo0 = 0xD2511F53u * c.x, hi0 = __umulhi(0xD2511F53u, c.x);
-    const uint32_t lo1 = 0xCD9E8D57u * c.z, hi1 = __umulhi(0xCD9E8D57u, c.z);
-    c = make_uint4(hi1 ^ c.y ^ k0, lo1, hi0 ^ c.w ^ k1, lo0);
-    k0 += 0x9E3779B9u;
-    k1 += 0xBB67AE85u;
-  }
-  return c;
-}
-
 // Gumbel term in log2 units: -log2(E log2 e) with E = -ln U,
 // U = ((w >> 8) + 0.5) / 2^24.  Near U = 1 (where the largest Gumbel values
 // come from) E is computed from t = 1 - U, which is exact in fp32, by the

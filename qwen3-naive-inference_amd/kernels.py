@@ -443,6 +443,76 @@ def sample_tokens(logits: torch.Tensor, temperature: float = 1.0, seed: int | No
     return tok, lp
 
 
+def _lm_head_args(hidden: torch.Tensor, weight: torch.Tensor):
+    for n, t in (("hidden", hidden), ("weight", weight)):
+        _require_cuda(n, t)
+        _require_dtype(n, t, torch.bfloat16)
+    if hidden.dim() != 2 or weight.dim() != 2 or hidden.shape[1] != weight.shape[1]:
+        raise ValueError(f"hidden [N, H] and weight [V, H] must share H, got {tuple(hidden.shape)} "
+                         f"and {tuple(weight.shape)}")
+    if hidden.shape[1] % 64:
+        raise ValueError(f"hidden size must be a multiple of 64, got {hidden.shape[1]}")
+    if weight.stride(1) != 1 or weight.stride(0) % 8 or weight.data_ptr() % 16:
+        raise ValueError("weight rows must be contiguous, 16-byte aligned, stride % 8 == 0")
+    if hidden.stride(1) != 1 or hidden.stride(0) % 8 or hidden.data_ptr() % 16:
+        hidden = hidden.contiguous()
+    n, hdim = hidden.shape
+    v = weight.shape[0]
+    nbytes = lib().qmi_lm_head_workspace_bytes(n, v)
+    ws = torch.empty((max(nbytes, 16) + 15) // 16 * 16, dtype=torch.uint8, device=hidden.device)
+    return hidden, n, v, hdim, ws
+
+
+def lm_head_sample(hidden: torch.Tensor, weight: torch.Tensor, temperature: float = 1.0,
+                   seed: int | None = None, offset: int = 0, want_logprobs: bool = True):
+    """``logits = hidden @ weight.T`` (fp32, never materialised), then one token
+    per row drawn from ``softmax(logits / temperature)`` and its log-probability
+    (qwen3_naive.py:1387 / :1607 lm_head, :1413-1423 / :1636-1650 sampling,
+    top_k = None).  Returns ``(tokens int64 [N], logprobs fp32 [N] or None)``.
+
+    The draw is inverse transform sampling with one Philox4x32-10 uniform per
+    row (counter (0, row, offset), key seed); ``seed`` defaults to a draw from
+    torch's default CPU generator, so ``torch.manual_seed`` makes the tokens
+    reproducible."""
+    if not (temperature > 0.0) or temperature == float("inf"):
+        raise ValueError(f"temperature must be finite and > 0, got {temperature}")
+    hidden, n, v, hdim, ws = _lm_head_args(hidden, weight)
+    if seed is None:
+        seed = int(torch.randint(0, 2 ** 62, (1,)).item())
+    tok = torch.empty((n,), dtype=torch.int64, device=hidden.device)
+    lp = torch.empty((n,), dtype=torch.float32, device=hidden.device) if want_logprobs else None
+    if n == 0:
+        return tok, lp
+    st = lib().qmi_lm_head_sample(hidden.data_ptr(), hidden.stride(0), n, weight.data_ptr(),
+                                  weight.stride(0), v, hdim, float(temperature),
+                                  int(seed) & (2 ** 64 - 1), int(offset) & (2 ** 64 - 1),
+                                  tok.data_ptr(), _ptr(lp), ws.data_ptr(), ws.numel(),
+                                  stream_handle(hidden.device))
+    check(st, "lm_head_sample")
+    return tok, lp
+
+
+def lm_head_logprob(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Tensor):
+    """``log_softmax(hidden @ weight.T)[targets]`` per row without materialising
+    the logits (lm_head + qwen3_grpo_train.py:46-53's gather).  ``targets``:
+    int64 ``[N]``.  Returns ``(logprobs fp32 [N], lse fp32 [N])``."""
+    hidden, n, v, hdim, ws = _lm_head_args(hidden, weight)
+    _require_cuda("targets", targets)
+    tg = targets.reshape(-1).to(torch.int64)
+    if tg.shape[0] != n:
+        raise ValueError(f"targets must have {n} entries, got {tg.shape[0]}")
+    lp = torch.empty((n,), dtype=torch.float32, device=hidden.device)
+    lse = torch.empty_like(lp)
+    if n == 0:
+        return lp, lse
+    st = lib().qmi_lm_head_logprob(hidden.data_ptr(), hidden.stride(0), n, weight.data_ptr(),
+                                   weight.stride(0), v, hdim, tg.data_ptr(), tg.stride(0),
+                                   lp.data_ptr(), lse.data_ptr(), ws.data_ptr(), ws.numel(),
+                                   stream_handle(hidden.device))
+    check(st, "lm_head_logprob")
+    return lp, lse
+
+
 def logprob_gather_backward(logits: torch.Tensor, ids: torch.Tensor, lse: torch.Tensor,
                             coef: torch.Tensor, grad_scale: torch.Tensor | None = None,
                             out: torch.Tensor | None = None) -> torch.Tensor:

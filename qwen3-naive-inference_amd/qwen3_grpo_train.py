@@ -7,7 +7,9 @@ qwen3-naive-inference's qwen3_grpo_train.py:
   grpo_train_step(model, optimizer, input_ids, old_log_probs, response_mask,
                   rewards, prompt_ids)               :261-286
 
-plus the fused path ``grpo_fused_loss`` / ``grpo_fused_train_step``: one
+plus the fused paths.  ``grpo_loss_from_hidden`` (and ``forward_logprob``
+without autograd) run the lm_head inside the log-softmax kernel, so no logits
+exist at all.  ``grpo_fused_loss`` / ``grpo_fused_train_step``: one
 streaming pass over the bf16 logits computes every token's log-probability,
 the group advantages and the clipped masked loss, and its backward writes the
 bf16 logit gradients directly, so the fp32 ``[B, T, V]`` log-softmax the
@@ -84,9 +86,41 @@ class PpoClippedLoss(torch.autograd.Function):
 # ---------------------------------------------------------------------------
 def forward_logprob(model, input_ids):
     """Per-position log-probability of ``input_ids`` under ``model`` (unshifted,
-    as the reference gathers position t's logits at token t)."""
+    as the reference gathers position t's logits at token t).
+
+    Without autograd the lm_head and the gather run fused (``lm_head_logprob``:
+    fp32 logits, never materialised); with autograd the bf16 logits are
+    materialised and the gather has a HIP backward."""
+    weight = getattr(getattr(model, "lm_head", None), "weight", None)
+    if (not torch.is_grad_enabled() and weight is not None and weight.is_cuda
+            and weight.dtype == torch.bfloat16 and hasattr(model, "model")):
+        hidden = model.model(input_ids)
+        lp, _ = K.lm_head_logprob(hidden.reshape(-1, hidden.shape[-1]), weight,
+                                  input_ids.reshape(-1))
+        return lp.view(input_ids.shape)
     logits = model(input_ids)
     return LogprobGather.apply(logits, input_ids)
+
+
+def grpo_loss_from_hidden(hidden, lm_head_weight, ids, old_log_probs, response_mask, rewards,
+                          prompt_ids, adv_eps: float = ADV_EPS,
+                          clip_epsilon: float = CLIP_EPSILON, reduction: str = "token",
+                          shift: bool = False):
+    """Forward-only GRPO loss step from final hidden states ``[B, T, H]``: each
+    token's log-probability by the fused lm_head kernel (the ``[B, T, V]``
+    logits never exist), group advantages and the clipped masked loss.
+    Returns (loss, lp ``[B, T']``, adv ``[B]``); ``shift`` as in grpo_fused_loss."""
+    if shift:
+        hidden, ids = hidden[:, :-1], ids[:, 1:]
+        old_log_probs = old_log_probs[:, 1:]
+        response_mask = response_mask[:, 1:]
+    bsz, t = ids.shape
+    lp, _ = K.lm_head_logprob(hidden.reshape(bsz * t, -1), lm_head_weight, ids.reshape(-1))
+    lp = lp.view(bsz, t)
+    adv = K.grpo_advantage(rewards, prompt_ids, adv_eps)
+    loss, _ = K.ppo_clipped_loss_fwd(lp, old_log_probs.float(), adv, response_mask.float(),
+                                     clip_epsilon, reduction, need_grad=False)
+    return loss, lp, adv
 
 
 def compute_grpo_advantage(rewards, prompt_ids, eps: float = ADV_EPS):

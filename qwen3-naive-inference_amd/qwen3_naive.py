@@ -619,16 +619,19 @@ class Qwen3ForCausalLM(nn.Module):
             budget -= seq.num_scheduled_tokens
         return scheduled
 
-    def _sample(self, logits, temperature, top_k, want_logprobs):
-        """Temperature / top-k / softmax / multinomial (qwen3_naive.py:1413-1423) and,
-        optionally, the sampled tokens' log-probabilities (:1649-1650).
+    def _sample(self, h, temperature, top_k, want_logprobs):
+        """lm_head + temperature / top-k / softmax / multinomial (qwen3_naive.py:1387,
+        :1413-1423) and, optionally, the sampled tokens' log-probabilities
+        (:1649-1650), from the final hidden states ``h`` of the sampled rows.
 
-        Without top-k the fused HIP sampler draws the tokens (Gumbel-max over
-        Philox uniforms, seeded from torch's CPU generator) and returns their
-        log-probabilities in the same pass over the bf16 logits."""
-        if top_k is None and logits.dtype == torch.bfloat16:
-            return K.sample_tokens(logits, temperature, want_logprobs=want_logprobs)
-        x = logits.float()
+        Without top-k the fused HIP kernel computes the logits in fp32 inside
+        the sampler (they are never materialised) and draws each token by
+        inverse transform sampling with one Philox uniform per row, seeded from
+        torch's CPU generator."""
+        w = self.lm_head.weight
+        if top_k is None and h.dtype == torch.bfloat16 and h.is_cuda and w.dtype == torch.bfloat16:
+            return K.lm_head_sample(h, w, temperature, want_logprobs=want_logprobs)
+        x = self.lm_head(h).float()
         if temperature != 1.0:
             x = x / temperature
         if top_k is not None:
@@ -716,7 +719,7 @@ class Qwen3ForCausalLM(nn.Module):
                     if ids_dev is not None:
                         ids = ids_dev
                     h = self.model.forward_decode(ids, pos, ctx, bt, slots)
-                nxt, lp = self._sample(self.lm_head(h), temperature, top_k, with_logprobs)
+                nxt, lp = self._sample(h, temperature, top_k, with_logprobs)
                 n = len(scheduled)
                 tok_host = torch.empty((n,), dtype=torch.int64, pin_memory=True)
                 tok_host.copy_(nxt, non_blocking=True)
@@ -771,7 +774,7 @@ class Qwen3ForCausalLM(nn.Module):
                     s.num_scheduled_tokens = 0
                 continue
             hs = h if sample_idx is None else h[torch.tensor(sample_idx, device=h.device)]
-            nxt, lp = self._sample(self.lm_head(hs), temperature, top_k, with_logprobs)
+            nxt, lp = self._sample(hs, temperature, top_k, with_logprobs)
             toks = nxt.tolist()
             lps = lp.tolist() if lp is not None else None
             sampled = [s for s in scheduled if s.num_scheduled_tokens == 1 or s.kv_len >= s.num_prompt_tokens]

@@ -50,3 +50,37 @@ def test_logprob_of_is_log_softmax():
     assert torch.allclose(lp, want, atol=1e-12)
     # probabilities of a row sum to one
     assert torch.allclose(OS.probs(logits, 0.8).sum(-1), torch.ones(4, dtype=torch.float64))
+
+
+def test_uniform53_layout_and_range():
+    u = OS.uniform53(5, seed=(9 << 32) | 5, offset=(3 << 32) | 7)
+    assert u.shape == (5,) and (u > 0).all() and (u < 1).all()
+    w = OS.philox4x32_10(np.array([[0, 3, 7, 3]], dtype=np.uint32), (5, 9))[0]
+    want = (((int(w[0]) << 21) | (int(w[1]) >> 11)) + 0.5) / 2 ** 53
+    assert u[3] == want
+    assert len(set(u.tolist())) == 5
+
+
+def test_inverse_cdf_closed_forms():
+    # p = softmax([0, 0]) = (1/2, 1/2): u below 1/2 draws 0, above draws 1.
+    x = torch.zeros(2, 2)
+    assert OS.inverse_cdf_draw(x, 1.0, np.array([0.25, 0.75])).tolist() == [0, 1]
+    # p = (1/6, 2/6, 3/6): boundaries at 1/6 and 1/2.
+    x = torch.log(torch.tensor([[1.0, 2.0, 3.0]])).expand(4, -1)
+    got = OS.inverse_cdf_draw(x, 1.0, np.array([0.1, 0.2, 0.49, 0.51]))
+    assert got.tolist() == [0, 1, 1, 2]
+    # Entries of zero probability are never drawn, even for u next to 1.
+    x = torch.tensor([[0.0, 1.0, float("-inf")]])
+    assert OS.inverse_cdf_draw(x, 1.0, np.array([1 - 2 ** -53])).tolist() == [1]
+
+
+def test_inverse_cdf_matches_softmax_frequencies():
+    logits = torch.tensor([[2.0, 1.0, 0.5, 0.0, -1.0, 3.0]]).to(torch.bfloat16)
+    n = 40000
+    for temp in (1.0, 0.7):
+        u = OS.uniform53(n, seed=13, offset=5)
+        tok = OS.inverse_cdf_draw(logits.expand(n, -1).contiguous(), temp, u)
+        counts = np.bincount(tok, minlength=6)
+        p = OS.probs(logits, temp)[0].numpy()
+        chi2 = ((counts - n * p) ** 2 / (n * p)).sum()
+        assert chi2 < stats.chi2.ppf(0.999, df=5), (temp, chi2, counts, n * p)
