@@ -372,6 +372,24 @@ int qmi_sample_tokens(const uint16_t* logits, int64_t row_stride, int64_t n_rows
                       float* out_logprobs, void* stream);
 
 /*
+ * Top-k token sampling from bf16 logits with the drawn token's log-probability.
+ * Replaces, for top_k = k, the sampling step of generate_continuous
+ * (qwen3_naive.py:1413-1422, the reference default k = 20) and of
+ * generate_continuous_with_logprobs (:1641-1650):
+ *   x = logits.float() / T; keep the k largest of x (the rest -inf);
+ *   tok ~ Categorical(softmax(x)); lp = log_softmax(x)[tok].
+ * Of entries tied at the k-th largest value the lowest indices are kept.
+ * Draw: inverse transform sampling over the kept entries in vocabulary order
+ * with u as in qmi_lm_head_sample (Philox4x32-10, counter (0, row, offset)).
+ * logits: [n_rows, vocab] bf16 (row stride row_stride); 1 <= top_k <= 1024
+ * and <= vocab.  out_tokens int64 [n_rows]; out_logprobs fp32 or NULL.
+ */
+int qmi_sample_tokens_topk(const uint16_t* logits, int64_t row_stride, int64_t n_rows,
+                           int64_t vocab, int64_t top_k, float temperature, uint64_t seed,
+                           uint64_t offset, int64_t* out_tokens, float* out_logprobs,
+                           void* stream);
+
+/*
  * Fused lm_head + sampling: logits = hidden_states . weight^T accumulated in
  * fp32 and never materialised, then one token per row drawn from
  * softmax(logits / temperature) with its log-probability.  Replaces

@@ -99,3 +99,38 @@ def inverse_cdf_draw(logits: torch.Tensor, temperature: float, u: np.ndarray) ->
     idx = np.array([np.searchsorted(cdf[r], u[r], side="right") for r in range(p.shape[0])])
     last = np.array([np.flatnonzero(p[r] > 0)[-1] for r in range(p.shape[0])])
     return np.minimum(idx, last)
+
+
+# ---------------------------------------------------------------------------
+# Top-k (qwen3_naive.py:1413-1422, :1641-1650): keep the k largest of
+# x = logits.float() / T, the rest -inf; softmax; draw; log_softmax at the draw.
+# Ties at the k-th value keep the lowest indices.
+
+def topk_mask(logits: torch.Tensor, k: int) -> np.ndarray:
+    """Boolean [N, V]: the k kept entries of each row (value descending, then
+    index ascending)."""
+    x = logits.float().numpy()
+    n, v = x.shape
+    keep = np.zeros((n, v), dtype=bool)
+    for r in range(n):
+        order = np.lexsort((np.arange(v), -x[r]))   # by -x, then index
+        keep[r, order[:k]] = True
+    return keep
+
+
+def topk_logprobs(logits: torch.Tensor, k: int, temperature: float) -> torch.Tensor:
+    """log_softmax of the top-k-filtered x / T (float64; -inf off the set)."""
+    keep = torch.from_numpy(topk_mask(logits, k))
+    x = logits.double() / temperature
+    x = x.masked_fill(~keep, float("-inf"))
+    return torch.log_softmax(x, dim=-1)
+
+
+def topk_inverse_cdf_draw(logits: torch.Tensor, k: int, temperature: float,
+                          u: np.ndarray) -> np.ndarray:
+    """First kept index (vocabulary order) whose cumulative top-k probability exceeds u."""
+    p = topk_logprobs(logits, k, temperature).exp().numpy()
+    cdf = np.cumsum(p, axis=-1)
+    idx = np.array([np.searchsorted(cdf[r], u[r], side="right") for r in range(p.shape[0])])
+    last = np.array([np.flatnonzero(p[r] > 0)[-1] for r in range(p.shape[0])])
+    return np.minimum(idx, last)

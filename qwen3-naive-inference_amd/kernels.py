@@ -443,6 +443,36 @@ def sample_tokens(logits: torch.Tensor, temperature: float = 1.0, seed: int | No
     return tok, lp
 
 
+def sample_tokens_topk(logits: torch.Tensor, top_k: int, temperature: float = 1.0,
+                       seed: int | None = None, offset: int = 0, want_logprobs: bool = True):
+    """Top-k sampling (qwen3_naive.py:1413-1422 / :1641-1650): keep the ``top_k``
+    largest of ``logits.float() / temperature`` per row, draw from their softmax
+    and return ``(tokens int64 [N], log-probabilities fp32 [N] or None)``.  Of
+    entries tied at the k-th value the lowest indices are kept.  ``seed``
+    defaults to a draw from torch's default CPU generator."""
+    _require_cuda("logits", logits)
+    _require_dtype("logits", logits, torch.bfloat16)
+    if logits.dim() != 2:
+        raise ValueError(f"logits must be [N, V], got {tuple(logits.shape)}")
+    n, v = logits.shape
+    if not 1 <= int(top_k) <= min(v, 1024):
+        raise ValueError(f"top_k must be in [1, min(vocab, 1024)], got {top_k}")
+    if not (temperature > 0.0) or temperature == float("inf"):
+        raise ValueError(f"temperature must be finite and > 0, got {temperature}")
+    if logits.stride(1) != 1:
+        logits = logits.contiguous()
+    if seed is None:
+        seed = int(torch.randint(0, 2 ** 62, (1,)).item())
+    tok = torch.empty((n,), dtype=torch.int64, device=logits.device)
+    lp = torch.empty((n,), dtype=torch.float32, device=logits.device) if want_logprobs else None
+    st = lib().qmi_sample_tokens_topk(logits.data_ptr(), logits.stride(0), n, v, int(top_k),
+                                      float(temperature), int(seed) & (2 ** 64 - 1),
+                                      int(offset) & (2 ** 64 - 1), tok.data_ptr(), _ptr(lp),
+                                      stream_handle(logits.device))
+    check(st, "sample_tokens_topk")
+    return tok, lp
+
+
 def _lm_head_args(hidden: torch.Tensor, weight: torch.Tensor):
     for n, t in (("hidden", hidden), ("weight", weight)):
         _require_cuda(n, t)

@@ -627,10 +627,17 @@ class Qwen3ForCausalLM(nn.Module):
         Without top-k the fused HIP kernel computes the logits in fp32 inside
         the sampler (they are never materialised) and draws each token by
         inverse transform sampling with one Philox uniform per row, seeded from
-        torch's CPU generator."""
+        torch's CPU generator; with top-k the bf16 logits are materialised and
+        a HIP radix-select sampler keeps the k largest and draws among them."""
         w = self.lm_head.weight
-        if top_k is None and h.dtype == torch.bfloat16 and h.is_cuda and w.dtype == torch.bfloat16:
+        if top_k is not None and top_k >= w.shape[0]:
+            top_k = None  # keeping every entry is plain sampling
+        kern = h.dtype == torch.bfloat16 and h.is_cuda and w.dtype == torch.bfloat16
+        if top_k is None and kern:
             return K.lm_head_sample(h, w, temperature, want_logprobs=want_logprobs)
+        if kern and top_k <= 1024:
+            return K.sample_tokens_topk(self.lm_head(h), top_k, temperature,
+                                        want_logprobs=want_logprobs)
         x = self.lm_head(h).float()
         if temperature != 1.0:
             x = x / temperature

@@ -88,3 +88,55 @@ def test_sample_rejects_bad_arguments(pkg, gpu):
             pkg.kernels.sample_tokens(lg, t)
     with pytest.raises(ValueError):
         pkg.kernels.sample_tokens(lg.float(), 1.0)
+
+
+@pytest.mark.parametrize("n,vocab,k,temp", [(1, 1000, 1, 1.0), (8, 1000, 20, 0.6),
+                                            (64, 151936, 20, 0.6), (256, 151936, 20, 1.0),
+                                            (16, 5000, 1000, 1.0), (5, 40, 40, 0.9)])
+def test_topk_sampler_matches_oracle(pkg, gpu, n, vocab, k, temp):
+    """Top-k sampling (the reference's default k = 20) against the oracle: the
+    same kept set (ties at the k-th value keep the lowest indices), the same
+    inverse-CDF draw for the same per-row uniform, log-probs to 1e-4."""
+    g = torch.Generator().manual_seed(n * 31 + k)
+    # bf16 logits of std 3: many ties at the k-th value across 151,936 entries.
+    logits = (3 * torch.randn(n, vocab, generator=g)).to(torch.bfloat16)
+    seed, offset = 99 + n, 5
+    print(f"[topk] n={n} vocab={vocab} k={k} T={temp}", flush=True)
+    tok, lp = pkg.kernels.sample_tokens_topk(logits.to(gpu), k, temp, seed=seed, offset=offset)
+    torch.cuda.synchronize()
+    tok, lp = tok.cpu(), lp.cpu()
+    keep = OS.topk_mask(logits, k)
+    assert keep[np.arange(n), tok.numpy()].all()
+    want = OS.topk_inverse_cdf_draw(logits, k, temp, OS.uniform53(n, seed, offset))
+    assert (tok.numpy() == want).mean() >= 0.99, (tok.numpy(), want)
+    ref = OS.topk_logprobs(logits, k, temp).gather(-1, tok[:, None])[:, 0]
+    assert ((lp.double() - ref).abs() / ref.abs().clamp_min(1.0)).max().item() <= 1e-4
+
+
+def test_topk_engine_path(pkg, gpu):
+    """generate_continuous with the reference's default top_k = 20 runs the HIP
+    top-k sampler: every generated token is among the most likely under the
+    model's own logits at that position (the batch forward's bf16 logits may
+    order the entries near the 20th slightly differently, hence 24)."""
+    cfg = pkg.Qwen3Config(num_hidden_layers=2, vocab_size=2048, tie_word_embeddings=False)
+    torch.manual_seed(0)
+    m = pkg.Qwen3ForCausalLM(cfg)
+    with torch.no_grad():
+        for name, p in m.named_parameters():
+            if "norm" in name:
+                p.fill_(1.0)
+            else:
+                p.normal_(0, 0.1)
+    m = m.to(gpu).to(torch.bfloat16).eval()
+    m.allocate_global_kv_cache(num_blocks=16)
+    prompts = [torch.randint(0, 2048, (1, 30), generator=torch.Generator().manual_seed(2))]
+    toks, gen, lps, _ = m.generate_continuous_with_logprobs(prompts, max_new_tokens=8,
+                                                            temperature=0.7, top_k=20)
+    seq = torch.tensor(toks[0], device=gpu)[None]
+    with torch.no_grad():
+        logits = m(seq)[0].float()
+    for j, t in enumerate(gen[0]):
+        row = logits[30 + j - 1]
+        assert t in torch.topk(row, 24).indices.tolist()
+        lp_ref = torch.log_softmax(torch.topk(row / 0.7, 20).values, -1)
+        assert lps[0][j] <= 0.0 and lps[0][j] >= lp_ref.min().item() - 0.1

@@ -84,3 +84,41 @@ def test_inverse_cdf_matches_softmax_frequencies():
         p = OS.probs(logits, temp)[0].numpy()
         chi2 = ((counts - n * p) ** 2 / (n * p)).sum()
         assert chi2 < stats.chi2.ppf(0.999, df=5), (temp, chi2, counts, n * p)
+
+
+def test_topk_set_matches_torch_topk_without_ties():
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(6, 500, generator=g, dtype=torch.float64).float()   # distinct values
+    keep = OS.topk_mask(x, 20)
+    want = torch.zeros_like(x, dtype=torch.bool).scatter(-1, torch.topk(x, 20).indices, True)
+    assert (keep == want.numpy()).all() and keep.sum(1).tolist() == [20] * 6
+
+
+def test_topk_ties_keep_lowest_indices_and_closed_forms():
+    x = torch.tensor([[1.0, 3.0, 2.0, 3.0, 2.0, 2.0, 0.0]])
+    assert np.flatnonzero(OS.topk_mask(x, 3)[0]).tolist() == [1, 2, 3]   # 3, 3 then the first 2
+    # k = 1 always draws the (first) maximum, with log-prob 0.
+    assert OS.topk_inverse_cdf_draw(x, 1, 0.7, np.array([0.999])).tolist() == [1]
+    assert OS.topk_logprobs(x, 1, 0.7)[0, 1].item() == 0.0
+    # k = V is plain sampling.
+    u = np.array([0.3])
+    assert OS.topk_inverse_cdf_draw(x, 7, 1.0, u).tolist() == OS.inverse_cdf_draw(x, 1.0, u).tolist()
+    # Two kept entries of logits 3 and 3 - ln 3: probabilities 3/4 and 1/4.
+    y = torch.tensor([[3.0, 3.0 - float(np.log(3.0)), -5.0]])
+    lp = OS.topk_logprobs(y, 2, 1.0)[0]
+    # (the logits are fp32: 3 - ln 3 carries one fp32 rounding)
+    assert abs(lp[0].item() - np.log(0.75)) < 1e-7 and abs(lp[1].item() - np.log(0.25)) < 1e-7
+    assert OS.topk_inverse_cdf_draw(y.expand(2, -1), 2, 1.0, np.array([0.74, 0.76])).tolist() == [0, 1]
+
+
+def test_topk_draw_frequencies():
+    logits = torch.tensor([[2.0, 1.0, 0.5, 0.0, -1.0, 3.0, 2.5, -0.5]]).to(torch.bfloat16)
+    n = 40000
+    u = OS.uniform53(n, seed=21, offset=9)
+    tok = OS.topk_inverse_cdf_draw(logits.expand(n, -1).contiguous(), 4, 0.8, u)
+    p = OS.topk_logprobs(logits, 4, 0.8)[0].exp().numpy()
+    counts = np.bincount(tok, minlength=8)
+    assert counts[p == 0].sum() == 0
+    kept = p > 0
+    chi2 = ((counts[kept] - n * p[kept]) ** 2 / (n * p[kept])).sum()
+    assert chi2 < stats.chi2.ppf(0.999, df=kept.sum() - 1)
