@@ -23,11 +23,13 @@
 //     query l%16) is exactly the B-operand layout of the second product
 //     O^T = V^T P^T once two 16-key blocks are packed to bf16, so P never
 //     leaves registers.
-//   * K and V tiles are staged through registers: each lane loads its
-//     16-byte chunks of the next tile from the page (8 per tile) once the
-//     current tile's QK product is done (so the staging registers are not
-//     live beside the K operands), then writes them to LDS at the end of the
-//     tile (ds_write_b128, a wave-wide write fills 1 KB, lane l at base + 16 l).
+//   * K and V tiles go from the page straight into LDS: gfx950's
+//     global_load_lds_dwordx4 (8 per lane per tile, no registers) writes a
+//     wave's 64 x 16 bytes to 1 KB of LDS, lane l at base + 16 l.  They are
+//     issued as inline asm at the start of the previous tile, so a tile's
+//     loads have a whole tile of compute to land, and the compiler puts no
+//     wait of its own on them (it cannot tell the LDS targets apart and
+//     would wait for every load in flight before each LDS access).
 //     Rows are 256 bytes (one KV head of a token) with the 16-byte chunks
 //     XOR-swizzled instead of padded: chunk c of K row r sits at c ^ (r % 16)
 //     (16 consecutive rows then hit 16 distinct 4-bank groups for the A
@@ -50,10 +52,12 @@
 //     is all ones), so it sums exactly the bf16 P the O^T product uses and
 //     costs no VALU adds.
 //   * K / V tiles of 64 keys (one quarter page) are double-buffered in LDS:
-//     the global loads of tile t+1 are in flight while tile t is computed,
-//     and their LDS writes go to the buffer no wave reads during tile t.
-//     Keys past the workgroup's last visible key are stale page rows: their
-//     scores are masked and their V rows are written to LDS as zeros.
+//     the loads of tile t+1 are in flight while tile t is computed and land
+//     in the buffer no wave reads during tile t; each wave waits for its own
+//     loads (s_waitcnt vmcnt(0)) before the tile's closing barrier.  Keys
+//     past the workgroup's last visible key are stale page rows: their
+//     scores are masked and their V rows are overwritten with zeros once
+//     they have landed.
 //   * Grid = (Hkv, B, query blocks): with 8 KV heads the KV head maps to the
 //     XCD, so all query blocks of one (sequence, KV head) share an L2.
 //     Query blocks are the slowest grid dimension and are issued last-first:
@@ -116,6 +120,18 @@ __device__ __forceinline__ u4v_t ds_read_b128_at(uint32_t addr) {
 template <int N>
 __device__ __forceinline__ void lgkm_wait_u4(u4v_t& a, u4v_t& b, u4v_t& c, u4v_t& d) {
   asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "i"(N) : "memory");
+}
+
+// Direct global -> LDS load of 16 bytes per lane (global_load_lds_dwordx4):
+// lane l's bytes at gbase + voff land at LDS byte lds + 16 l.  Inline asm, so
+// that the compiler adds no wait for it (it cannot tell the LDS targets
+// apart and would wait for every outstanding load); the caller waits with
+// s_waitcnt vmcnt.
+__device__ __forceinline__ void lds_load16(const void* gbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :
+               : "s"(lds), "v"(voff), "s"(gbase)
+               : "memory", "m0");
 }
 
 // Calls f(std::integral_constant<int, i>) for i = I .. N-1.
@@ -228,15 +244,10 @@ void varlen_prefill_kernel(
   // zeroed.  A tile whose page-table entry is outside [0, num_blocks) is
   // skipped in the compute.
   const int64_t row_elems = (int64_t)num_kv_heads * kHeadDim;
-  // Tiles are staged through registers: at the start of tile t every lane
-  // loads its 16-byte chunks of tile t+1 (4 of K, 4 of V) into registers, and
-  // after tile t's compute writes them to the other LDS buffer.  (The gfx950
-  // direct global -> LDS loads cost ~30% of this kernel's time: their LDS
-  // writes hold up the waves' own LDS traffic, while the same bytes through
-  // registers and ds_write_b128 cost no measurable time.)  Chunk i of wave w
-  // covers rows 4q .. 4q+3 (q = 4w + i): lane l holds row 4q + l / 16,
-  // physical chunk l % 16 (fetched from the logical chunk the swizzle maps
-  // there) and writes it at byte 1024 q + 16 l of the buffer.
+  // Lane offsets of the tile loads: chunk i of wave w covers rows 4q .. 4q+3
+  // (q = 4w + i); lane l fetches row 4q + l / 16, physical chunk l % 16 (the
+  // logical chunk the swizzle maps there), which lands at byte 1024 q + 16 l
+  // of the buffer.
   uint32_t k_src[4], v_src[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -248,9 +259,9 @@ void varlen_prefill_kernel(
   // holds the entry of page pg0 + i (-1 past the table's width), read with
   // v_readlane, so the tile loop has no memory load besides the tile's own.
   int pg0 = 0, pg_lane = -1;
-  uint4 stg_k[4], stg_v[4];
   bool tile_ok[2] = {false, false};
   int st_valid[2] = {0, 0};
+  // Tile t into LDS buffer buf by direct loads (M0 = the wave's 1 KB block).
   auto load_tile = [&](int t, int buf) {
     const int key0 = t * kKeyTile;
     const int32_t blk = __builtin_amdgcn_readlane(pg_lane, key0 / kPage - pg0);
@@ -258,31 +269,31 @@ void varlen_prefill_kernel(
     const int64_t row0 = (int64_t)(page_ok ? blk : 0) * kPage + (key0 % kPage);
     const char* kb = reinterpret_cast<const char*>(k_cache + row0 * row_elems + kvh * kHeadDim);
     const char* vb = reinterpret_cast<const char*>(v_cache + row0 * row_elems + kvh * kHeadDim);
+    const uint32_t lk = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)&sK[buf][16 * wave * kHeadDim]);
+    const uint32_t lv = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)&sV[buf][16 * wave * kHeadDim]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      stg_k[i] = load_u4(kb + k_src[i]);
-      stg_v[i] = load_u4(vb + v_src[i]);
+      lds_load16(kb, k_src[i], lk + i * 4 * kHeadDim * 2);
+      lds_load16(vb, v_src[i], lv + i * 4 * kHeadDim * 2);
     }
     st_valid[buf] = page_ok ? min(kKeyTile, kend - key0) : 0;
     tile_ok[buf] = st_valid[buf] > 0;
   };
-  // Writes the staged tile to LDS buffer buf.  V rows past the valid keys are
-  // written as zeros (0 * a stale NaN would poison O); stale K rows are masked
-  // in the scores.
-  auto store_tile = [&](int buf) {
+  // Once tile buf has landed: V rows past the valid keys become zeros (0 * a
+  // stale NaN would poison O; stale K rows are masked in the scores).  Each
+  // wave clears the rows it loaded.
+  auto finish_tile = [&](int buf) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     const int valid = st_valid[buf];
     if (valid < kKeyTile) {  // wave-uniform: partial tiles only
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int row = 4 * (4 * wave + i) + (lane >> 4);
-        if (row >= valid) stg_v[i] = make_uint4(0, 0, 0, 0);
+        const int q4 = 4 * wave + i, row = 4 * q4 + (lane >> 4);
+        if (row >= valid)
+          *reinterpret_cast<uint4*>(&sV[buf][q4 * 4 * kHeadDim + 8 * lane]) = make_uint4(0, 0, 0, 0);
       }
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int q4 = 4 * wave + i;
-      *reinterpret_cast<uint4*>(&sK[buf][q4 * 4 * kHeadDim + 8 * lane]) = stg_k[i];
-      *reinterpret_cast<uint4*>(&sV[buf][q4 * 4 * kHeadDim + 8 * lane]) = stg_v[i];
     }
   };
 
@@ -330,6 +341,9 @@ void varlen_prefill_kernel(
   auto tile_step = [&](int t, int t_last, auto buf_c) __attribute__((always_inline)) {
     constexpr int buf = decltype(buf_c)::value;
     const bool compute = tile_ok[buf];  // wave-uniform
+    // The next tile's loads go out first: its buffer held tile t-1, done
+    // before the last barrier.
+    load_tile(min(t + 1, t_last), buf ^ 1);
     if (compute) {
 
     // ---- S^T = K Q^T for 4 blocks of 16 keys x 2 blocks of 16 queries ----
@@ -367,7 +381,6 @@ void varlen_prefill_kernel(
                                                                qop[j][c], s[j][kb], 0, 0, 0);
       });
     }
-    load_tile(min(t + 1, t_last), buf ^ 1);
 
     // ---- per query block: mask, online softmax, P^T packed to bf16 ----
     // Scores stay unscaled; p = exp2(s * scale_log2 - m).  The running max m
@@ -470,10 +483,8 @@ void varlen_prefill_kernel(
           for (int j = 0; j < 2; ++j)
             acc_l[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pop[j][c], acc_l[j], 0, 0, 0);
       }
-    } else {  // compute
-      load_tile(min(t + 1, t_last), buf ^ 1);
     }
-    store_tile(buf ^ 1);
+    finish_tile(buf ^ 1);
     __syncthreads();
   };
   // Segments of at most kSegTiles tiles span at most 61 pages, within the 64
@@ -483,8 +494,15 @@ void varlen_prefill_kernel(
     const int seg_last = min(t_end, seg + kSegTiles) - 1;
     pg0 = seg * kKeyTile / kPage;
     pg_lane = pg0 + lane < bt_width ? block_table[(int64_t)b * bt_stride + pg0 + lane] : -1;
+    // Consume the vector loads before the tile loop (page-table entries, Q
+    // rows), so the compiler's wait for them is not repeated on every tile.
+    asm volatile("" ::"v"(pg_lane));
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) asm volatile("" ::"v"(qop[j][c]));
     load_tile(seg, 0);
-    store_tile(0);
+    finish_tile(0);
     __syncthreads();
     for (int t = seg; t <= seg_last; t += 2) {
       tile_step(t, seg_last, std::integral_constant<int, 0>{});
