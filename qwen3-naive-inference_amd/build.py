@@ -10,6 +10,7 @@ Usage: ``python -m`` is not possible for this package directory name, so run
 from __future__ import annotations
 
 import concurrent.futures
+import importlib.util
 import os
 import shutil
 import subprocess
@@ -46,6 +47,11 @@ EXTRA_FLAGS = {
     "varlen_prefill.hip": ["-fno-honor-nans"],
 }
 
+# Sources whose kernels place LDS waits by hand (inline-asm LDS reads with
+# explicit lgkmcnt waits, inline-asm direct global->LDS loads through M0).
+# Their device assembly is checked on every build (asm_check.py).
+ASM_CHECKED = ("varlen_prefill.hip",)
+
 
 def hipcc_path() -> str:
     rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
@@ -78,10 +84,22 @@ def _compile(src: Path, verbose: bool) -> Path:
     return obj
 
 
+def _asm_check(src: Path) -> None:
+    spec = importlib.util.spec_from_file_location("qmi_asm_check", PKG_DIR / "asm_check.py")
+    asm_check = sys.modules.get(spec.name)
+    if asm_check is None:
+        asm_check = importlib.util.module_from_spec(spec)
+        sys.modules[spec.name] = asm_check
+        spec.loader.exec_module(asm_check)
+    asm_check.check_source(src, hipcc_path(), [*HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, [])])
+
+
 def build(verbose: bool = False, jobs: int | None = None) -> Path:
     """Compile every ``csrc/*.hip`` for gfx950 and link ``libqwen3mi.so``.
 
-    Always recompiles (this is the build check); returns the library path.
+    Always recompiles (this is the build check) and checks the hand-placed
+    LDS waits of the ``ASM_CHECKED`` sources in their device assembly;
+    returns the library path.
     """
     OBJ_DIR.mkdir(exist_ok=True)
     srcs = sources()
@@ -89,7 +107,10 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 4)), 16)
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as ex:
+        checks = [ex.submit(_asm_check, s) for s in srcs if s.name in ASM_CHECKED]
         objs = list(ex.map(lambda s: _compile(s, verbose), srcs))
+        for c in checks:
+            c.result()
     tmp = LIB_PATH.with_suffix(".so.tmp")
     cmd = [hipcc_path(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
            *map(str, objs)]
