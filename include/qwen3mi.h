@@ -156,18 +156,29 @@ int qmi_paged_decode_attention_noalloc(const uint16_t* q, int64_t q_seq_stride,
  * whose table entry is outside [0, num_blocks) contribute nothing (as in
  * decode); num_blocks == 0 is rejected (QMI_E_BAD_SHAPE).
  *
- * Long key ranges: key ranges can be split into pieces run by separate
- * workgroups, whose fp32 partial results go to `workspace` and are merged by
- * a second kernel on the same stream.  split_keys == 0 (automatic) splits
- * only launches with fewer than 256 (query block, sequence, KV head) work
- * items, e.g. a short chunk after a long cached prefix, into enough pieces
- * to give about 512 workgroups (at most 16 per item); split_keys > 0 (a
- * multiple of 64) cuts key ranges into pieces of that many keys (at most 16
- * per item) whatever the launch size.  max_seqlen_k (the longest Lk) only
- * sizes the split; any value gives the same result.  Pass a workspace of at
- * least qmi_varlen_prefill_workspace_bytes(...) bytes (16-byte aligned);
- * with a smaller one (or NULL) nothing is split.  Calls that share one
- * workspace must not overlap.
+ * Scheduling (split_keys == 0).  A work item is one (query block of 128 / G
+ * queries, sequence, KV head).  Launches with at least 256 and fewer than
+ * 4 per CU items run on a persistent grid (two workgroups per CU, each
+ * serving one KV head) that takes items from per-KV-head counters in the
+ * workspace, long causal blocks first; a thin launch (no more items per KV
+ * head than workgroups per head, e.g. a chunk after a long cached prefix)
+ * also cuts its long items into pieces of about two balanced shares, whose
+ * partial results (bf16 rows + fp32 max / sum) are merged by a second
+ * kernel on the same stream.  Launches with fewer than 256 items split key
+ * ranges across workgroups (fp32 partials, at most 16 pieces per item) and
+ * thicker ones run one workgroup per item.  split_keys > 0 (a multiple of
+ * 64) instead cuts key ranges into pieces of that many keys (at most 16 per
+ * item) whatever the launch size.  max_seqlen_k (the longest Lk) only sizes
+ * the split; any value gives the same result up to the rounding of merged
+ * pieces.
+ *
+ * Workspace: at least qmi_varlen_prefill_workspace_bytes(...) bytes,
+ * 16-byte aligned.  Its first bytes hold the work-queue counters: zero the
+ * workspace once before its first use (e.g. hipMemset after allocating it);
+ * every call leaves the counters at zero.  With a smaller workspace (or
+ * NULL) the persistent grid and all splits are off (one workgroup per item,
+ * same result).  Calls that share one workspace must not overlap (order
+ * them on one stream).
  */
 int64_t qmi_varlen_prefill_workspace_bytes(int64_t batch, int64_t max_seqlen_q,
                                            int64_t max_seqlen_k, int64_t num_q_heads,

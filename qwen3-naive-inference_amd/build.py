@@ -43,8 +43,13 @@ HIPCC_FLAGS = [
 # v_max_f32 x, x, x in front of every operand, with relaxed NaN handling the
 # chains become v_max3_f32.  That kernel never produces a NaN score from
 # finite inputs (stale page rows are masked to -inf before any maximum).
+#
+# The prefill kernel takes its next work-queue ticket with one atomic by one
+# thread and uses the value only after the next item's loads; the AMDGPU
+# atomic optimizer would rewrite that atomic into a wave-wide form whose
+# result is consumed (and waited for) at once.
 EXTRA_FLAGS = {
-    "varlen_prefill.hip": ["-fno-honor-nans"],
+    "varlen_prefill.hip": ["-fno-honor-nans", "-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
 }
 
 # Sources whose kernels place LDS waits by hand (inline-asm LDS reads with

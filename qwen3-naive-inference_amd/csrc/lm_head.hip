@@ -516,19 +516,6 @@ int check_args(const uint16_t* h, int64_t h_stride, int64_t n_rows, const uint16
   return QMI_OK;
 }
 
-int cu_count() {
-  static int cache[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cache[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-    cache[dev] = n;
-  }
-  return cache[dev];
-}
-
 int launch_tiles(const uint16_t* h, int64_t h_stride, int64_t n_rows, const uint16_t* w,
                  int64_t w_stride, int64_t vocab, int64_t hidden, float c2, const int64_t* tgt,
                  int64_t tgt_stride, const LmWs& ws, hipStream_t s) {
@@ -543,7 +530,7 @@ int launch_tiles(const uint16_t* h, int64_t h_stride, int64_t n_rows, const uint
   do {                                                                                            \
     const int nrt = (int)((n_rows + MT - 1) / MT);                                                \
     const int64_t tiles = (int64_t)nvt * nrt;                                                     \
-    const int64_t grid = std::min<int64_t>(tiles, (int64_t)cu_count() * PER_CU);                  \
+    const int64_t grid = std::min<int64_t>(tiles, (int64_t)device_cu_count() * PER_CU);           \
     hipLaunchKernelGGL((lmhead_tiles<MT, NW, NS>), dim3((unsigned)grid), dim3(NW * 64), 0, s, h,   \
                        h_stride, (int)n_rows, w, w_stride, (int)vocab, (int)hidden, c2, tgt,      \
                        tgt_stride, nvt, nrt, ws.part, ws.tgt_logit);                              \

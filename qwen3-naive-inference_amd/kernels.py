@@ -151,12 +151,35 @@ def paged_decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
 # ---------------------------------------------------------------------------
 # Varlen paged causal prefill (flash_attn_varlen_func at qwen3_naive.py:631-637)
 # ---------------------------------------------------------------------------
+# Per-device prefill workspace.  Its first bytes hold the work-queue counters
+# of the attention kernel, which must be zero before a launch and are left
+# zero by every launch, so it is zero-filled once when (re)allocated and then
+# reused; launches that share it run in stream order (torch's current stream).
+_PREFILL_WS: dict[int, torch.Tensor] = {}
+
+
+def _prefill_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    if torch.cuda.is_current_stream_capturing():
+        cached = _PREFILL_WS.get(device.index)
+        if cached is not None and cached.numel() * 4 >= nbytes:
+            return cached
+        # A buffer made during capture belongs to the graph's pool: zero-filled
+        # by a captured fill kernel on every replay, never cached.
+        return torch.zeros((nbytes + 3) // 4, dtype=torch.float32, device=device)
+    ws = _PREFILL_WS.get(device.index)
+    if ws is None or ws.numel() * 4 < nbytes:
+        ws = torch.zeros((nbytes + 3) // 4, dtype=torch.float32, device=device)
+        _PREFILL_WS[device.index] = ws
+    return ws
+
+
 def varlen_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                              cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor,
                              max_seqlen_q: int, max_seqlen_k: int, softmax_scale: float,
                              causal: bool = True, block_table: torch.Tensor | None = None,
                              out: torch.Tensor | None = None, *,
-                             split_keys: int = 0) -> torch.Tensor:
+                             split_keys: int = 0,
+                             workspace: torch.Tensor | None = None) -> torch.Tensor:
     """Varlen causal attention of the new tokens over their paged K/V.
 
     Argument order and meaning follow the reference call
@@ -167,11 +190,15 @@ def varlen_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: to
     ``block_table``: int32 ``[B, W]``.  Returns ``[Tq, Hq, 128]`` bf16.
     The kernel reads the per-sequence key counts from ``cu_seqlens_k``;
     ``max_seqlen_k`` only sizes the split of long key ranges across
-    workgroups: with ``split_keys=0`` launches with fewer than 256 (query
-    block, sequence, KV head) items are split automatically (e.g. a short
-    chunk after a long cached prefix); ``split_keys > 0`` forces pieces of
-    that many keys.  The fp32 partials go to a workspace from the torch
-    allocator and are merged by a second kernel.
+    workgroups.  With ``split_keys=0`` the library schedules the launch:
+    launches of a few rounds of (query block, sequence, KV head) items run on
+    a persistent grid fed by a work queue, thin ones (no more items per KV
+    head than workgroups) with their long items split and merged by a
+    second kernel, tiny ones (fewer than 256 items) split across workgroups;
+    ``split_keys > 0`` forces pieces of that many keys.  ``workspace``
+    (float32, at least ``qmi_varlen_prefill_workspace_bytes`` bytes, zeroed
+    before its first use and left zeroed by every call) defaults to one
+    cached per device.
     """
     if not causal:
         raise ValueError("only causal=True is supported (the reference always passes it)")
@@ -218,8 +245,15 @@ def varlen_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: to
         raise ValueError(f"split_keys must be 0 or a positive multiple of 64, got {split_keys}")
     ws_bytes = lib().qmi_varlen_prefill_workspace_bytes(
         bsz, int(max_seqlen_q), int(max_seqlen_k), hq, hkv, bt.shape[1], split_keys)
-    ws = (torch.empty(ws_bytes // 4, dtype=torch.float32, device=q.device) if ws_bytes > 0
-          else None)
+    if workspace is None:
+        ws = _prefill_workspace(q.device, ws_bytes) if ws_bytes > 0 else None
+    else:
+        _require_cuda("workspace", workspace)
+        _require_dtype("workspace", workspace, torch.float32)
+        if workspace.numel() * 4 < ws_bytes or not workspace.is_contiguous():
+            raise ValueError(f"workspace must be contiguous with at least {ws_bytes} bytes")
+        ws = workspace
+        ws_bytes = workspace.numel() * 4
     st = lib().qmi_varlen_prefill_attention(
         q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(), nb, bs,
         hq, hkv, d, cq.data_ptr(), ck.data_ptr(), bt.data_ptr(), bt.stride(0), bt.shape[1], bsz,

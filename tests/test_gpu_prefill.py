@@ -362,3 +362,52 @@ def test_prefill_misaligned_q_view(pkg, gpu):
                                                True, bt.to(gpu))
     torch.cuda.synchronize()
     _check(out, q, kc, vc, [0, L], [0, L], bt)
+
+
+@pytest.mark.parametrize("lens_q,prefix,hq,hkv", [
+    ([512] * 10, 1024, 16, 8),   # 80 items per KV head: work queue, no split
+    ([512] * 4, 2000, 16, 8),    # 32 items per KV head: thin, long items split
+    ([1024] * 2, 1500, 16, 4),   # GQA 4: 64 items per KV head, thin
+    ([512, 300, 512, 77, 512, 512, 200, 512], 1200, 8, 8),  # GQA 1, ragged chunks, thin
+])
+def test_prefill_queue_modes(pkg, gpu, lens_q, prefix, hq, hkv):
+    """Launches of a few rounds of items run on the persistent work queue
+    (thin ones with split items and the merge kernel): they match the oracle,
+    two calls on one zeroed workspace give identical results, and the
+    queue's counters are back at zero after each call."""
+    lens_k = [prefix + n for n in lens_q]
+    kc, vc, bt = _pool(90 + len(lens_q) + hq, lens_k, hkv=hkv)
+    cu_q, cu_k = [0], [0]
+    for a, c in zip(lens_q, lens_k):
+        cu_q.append(cu_q[-1] + a)
+        cu_k.append(cu_k[-1] + c)
+    g = torch.Generator().manual_seed(91 + hq)
+    q = torch.randn(cu_q[-1], hq, 128, generator=g).to(torch.bfloat16)
+    nbytes = pkg._lib.lib().qmi_varlen_prefill_workspace_bytes(len(lens_q), max(lens_q), max(lens_k),
+                                                               hq, hkv, bt.shape[1], 0)
+    ws = torch.zeros(nbytes // 4 + 1, dtype=torch.float32, device=gpu)
+    args = (q.to(gpu), kc.to(gpu), vc.to(gpu), torch.tensor(cu_q, dtype=torch.int32, device=gpu),
+            torch.tensor(cu_k, dtype=torch.int32, device=gpu), max(lens_q), max(lens_k), SCALE,
+            True, bt.to(gpu))
+    print(f"[prefill] queue mode {len(lens_q)} seqs prefix {prefix} gqa {hq}/{hkv}", flush=True)
+    out1 = pkg.kernels.varlen_prefill_attention(*args, workspace=ws)
+    torch.cuda.synchronize()
+    counters = ws[:hkv + 1].view(torch.int32).cpu()
+    assert int(counters.abs().sum()) == 0, counters
+    out2 = pkg.kernels.varlen_prefill_attention(*args, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(out1, out2)
+    assert int(ws[:hkv + 1].view(torch.int32).abs().sum().item()) == 0
+    _check(out1, q, kc, vc, cu_q, cu_k, bt)
+    # Without the workspace (C ABI, NULL): one workgroup per item, unsplit.
+    import ctypes
+    whole = torch.empty_like(out1)
+    qg, kcg, vcg, cqg, ckg, _, _, _, _, btg = args
+    st = pkg._lib.lib().qmi_varlen_prefill_attention(
+        qg.data_ptr(), qg.stride(0), qg.stride(1), kcg.data_ptr(), vcg.data_ptr(), kcg.shape[0], 256,
+        hq, hkv, 128, cqg.data_ptr(), ckg.data_ptr(), btg.data_ptr(), btg.stride(0), btg.shape[1],
+        len(lens_q), max(lens_q), max(lens_k), cu_q[-1], SCALE, whole.data_ptr(), whole.stride(0),
+        whole.stride(1), None, 0, 0, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    assert st == 0
+    assert (out1.float() - whole.float()).abs().max().item() <= 1e-2
