@@ -54,6 +54,16 @@ def load_pkg():
     return importlib.import_module("qwen3-naive-inference_amd")
 
 
+def warm_up(torch, fn_list, seconds):
+    """Run fn_list repeatedly for about ``seconds`` (untimed), so that a leg
+    that follows a CPU-only phase is timed at the GPU's running clocks."""
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end:
+        for fn in fn_list:
+            fn()
+        torch.cuda.synchronize()
+
+
 def timed_launches(torch, fn_list, steps, warmup):
     """Run ``warmup`` untimed steps, then ``steps`` timed steps.
 
@@ -522,6 +532,9 @@ def leg_prefill(torch, pkg, W, dev, steps, warmup, cpu=True):
     fns = [(lambda c=c: pkg.kernels.varlen_prefill_attention(
         c["q"], kc, vc, c["cu_seqlens_q"], c["cu_seqlens_k"], c["max_seqlen_q"],
         c["max_seqlen_k"], 128 ** -0.5, True, c["block_tables"])) for c in calls]
+    # The leg follows the KV-store leg's CPU baseline (the GPU idles for tens
+    # of seconds): half a second of its own launches first.
+    warm_up(torch, fns, 0.5)
     _, per = timed_launches(torch, fns, steps, warmup)
     # The layer's four launches back to back, with events only around the whole
     # timed region (events between launches add gaps the model does not have).
