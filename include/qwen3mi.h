@@ -265,6 +265,51 @@ int qmi_silu_mul(const uint16_t* gate_up, int64_t gate_up_stride, int64_t n_rows
                  uint16_t* out, int64_t out_stride, void* stream);
 
 /*
+ * Decode-batch projection y = x W^T (bf16 in and out, fp32 accumulation, one
+ * rounding per output) for at most 256 rows.  Replaces the bf16 nn.Linear
+ * calls of a decode step: qkv_proj (qwen3_naive.py:427, :654) and, with
+ * activation 1, gate_up_proj followed by silu(gate) * up (qwen3_naive.py:692,
+ * :699-701).  x [m, k] (row stride x_stride), w [n, k] (row stride w_stride),
+ * y [m, n] (row stride y_stride).  activation 1 (SwiGLU): w is the packed
+ * [2n, k] = [gate; up] weight and y[i, j] = bf16(silu(g) * u) with
+ * g = bf16(x_i . gate_j), u = bf16(x_i . up_j) — the rounding points of a bf16
+ * gate_up GEMM followed by qmi_silu_mul.  Requires m <= 256, k % 128 == 0,
+ * n % 16 == 0; x and w 16-byte aligned with strides % 8 == 0 (>= k); y
+ * 8-byte aligned, y_stride % 4 == 0 (>= n).
+ */
+int qmi_linear_rows(const uint16_t* x, int64_t x_stride, const uint16_t* w, int64_t w_stride,
+                    int64_t m, int64_t n, int64_t k, int32_t activation, uint16_t* y,
+                    int64_t y_stride, void* stream);
+
+/*
+ * Split-K form of qmi_linear_rows for the narrow projections that feed a
+ * residual add + RMSNorm (o_proj, qwen3_naive.py:428, :683; down_proj,
+ * :693, :702): writes parts[s][m][n] fp32 (contiguous) with
+ * sum_s parts[s] = x W^T, so that few rows still spread over the GPU.
+ * n_parts must equal qmi_linear_rows_parts_count(m, n, k) (0: unsupported
+ * shape).  Same layout rules as qmi_linear_rows; parts 16-byte aligned.
+ */
+int64_t qmi_linear_rows_parts_count(int64_t m, int64_t n, int64_t k);
+int qmi_linear_rows_parts(const uint16_t* x, int64_t x_stride, const uint16_t* w,
+                          int64_t w_stride, int64_t m, int64_t n, int64_t k, float* parts,
+                          int64_t n_parts, void* stream);
+
+/*
+ * Residual add + RMSNorm over a projection given as its partial products:
+ * x = bf16(sum_s parts[s]) (the projection's bf16 output), then as
+ * qmi_add_rms_norm: s = x + residual (fp32), residual_out = bf16(s),
+ * y = bf16(s * rsqrt(mean(s^2) + eps) * w).  Replaces the o_proj / down_proj
+ * output feeding RMSNorm._add_rms_norm (qwen3_naive.py:163-169).
+ * parts [n_parts][m][n] fp32 contiguous; n % 8 == 0, n <= 4096; rows and the
+ * weight 16-byte aligned with strides % 8 == 0.
+ */
+int qmi_add_rms_norm_parts(const float* parts, int64_t n_parts, int64_t m,
+                           const uint16_t* residual, int64_t residual_stride,
+                           uint16_t* residual_out, int64_t residual_out_stride,
+                           const uint16_t* weight, uint16_t* y, int64_t y_stride, int64_t n,
+                           float eps, void* stream);
+
+/*
  * Row-wise log-softmax gathered at one token per row.
  * Replaces `F.log_softmax(logits.float(), -1).gather(-1, ids)` of
  * forward_logprob (qwen3_grpo_train.py:46-53) and the rollout's

@@ -67,6 +67,13 @@ SIGNATURES: dict[str, tuple] = {
         _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_p,
         _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_f32, _c_p]),
     "qmi_silu_mul": (ctypes.c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p]),
+    "qmi_linear_rows": (ctypes.c_int, [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32,
+                                       _c_p, _c_i64, _c_p]),
+    "qmi_linear_rows_parts_count": (_c_i64, [_c_i64, _c_i64, _c_i64]),
+    "qmi_linear_rows_parts": (ctypes.c_int, [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
+                                             _c_p, _c_i64, _c_p]),
+    "qmi_add_rms_norm_parts": (ctypes.c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_i64,
+                                              _c_p, _c_p, _c_i64, _c_i64, _c_f32, _c_p]),
     "qmi_logprob_gather": (ctypes.c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i64,
                                           _c_i64, _c_i64, _c_p, _c_p, _c_p]),
     "qmi_grpo_advantage": (ctypes.c_int, [_c_p, _c_p, _c_i64, _c_f32, _c_p, _c_p]),

@@ -55,7 +55,7 @@ EXTRA_FLAGS = {
 # Sources whose kernels place LDS waits by hand (inline-asm LDS reads with
 # explicit lgkmcnt waits, inline-asm direct global->LDS loads through M0).
 # Their device assembly is checked on every build (asm_check.py).
-ASM_CHECKED = ("varlen_prefill.hip",)
+ASM_CHECKED = ("varlen_prefill.hip", "linear_rows.hip")
 
 
 def hipcc_path() -> str:
@@ -89,14 +89,18 @@ def _compile(src: Path, verbose: bool) -> Path:
     return obj
 
 
-def _asm_check(src: Path) -> None:
+def _load_asm_check():
     spec = importlib.util.spec_from_file_location("qmi_asm_check", PKG_DIR / "asm_check.py")
-    asm_check = sys.modules.get(spec.name)
-    if asm_check is None:
-        asm_check = importlib.util.module_from_spec(spec)
-        sys.modules[spec.name] = asm_check
-        spec.loader.exec_module(asm_check)
-    asm_check.check_source(src, hipcc_path(), [*HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, [])])
+    mod = sys.modules.get(spec.name)
+    if mod is None:
+        mod = importlib.util.module_from_spec(spec)
+        sys.modules[spec.name] = mod
+        spec.loader.exec_module(mod)
+    return mod
+
+
+def _asm_check(mod, src: Path) -> None:
+    mod.check_source(src, hipcc_path(), [*HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, [])])
 
 
 def build(verbose: bool = False, jobs: int | None = None) -> Path:
@@ -112,7 +116,8 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 4)), 16)
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as ex:
-        checks = [ex.submit(_asm_check, s) for s in srcs if s.name in ASM_CHECKED]
+        mod = _load_asm_check()
+        checks = [ex.submit(_asm_check, mod, s) for s in srcs if s.name in ASM_CHECKED]
         objs = list(ex.map(lambda s: _compile(s, verbose), srcs))
         for c in checks:
             c.result()

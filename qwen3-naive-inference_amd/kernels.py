@@ -409,6 +409,107 @@ def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
 
 
 # ---------------------------------------------------------------------------
+# Decode-batch projections (qwen3_naive.py:427-428, :654, :683, :692-702)
+# ---------------------------------------------------------------------------
+LINEAR_ROWS_MAX = 256
+
+
+class RowParts:
+    """A projection ``x W^T`` held as fp32 partial products ``parts [S, M, N]``
+    (their sum); the residual add + RMSNorm that follows consumes them
+    (``add_rms_norm_parts``)."""
+
+    __slots__ = ("parts",)
+
+    def __init__(self, parts: torch.Tensor):
+        self.parts = parts
+
+    @property
+    def shape(self):
+        return self.parts.shape[1:]
+
+    def dense(self) -> torch.Tensor:
+        """The projection's bf16 output (one rounding of the fp32 sum)."""
+        return self.parts.sum(0).to(torch.bfloat16)
+
+
+def linear_rows_ok(x: torch.Tensor, weight: torch.Tensor, swiglu: bool = False) -> bool:
+    """Whether ``qmi_linear_rows`` takes ``x [M, K] @ weight[N, K]^T``: bf16 GPU
+    tensors, 1 <= M <= 256, K % 128 == 0, output width % 16 == 0."""
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16 or x.dim() != 2:
+        return False
+    if not (x.is_cuda and weight.is_cuda) or weight.dim() != 2:
+        return False
+    n = weight.shape[0] // 2 if swiglu else weight.shape[0]
+    return (0 < x.shape[0] <= LINEAR_ROWS_MAX and x.shape[1] == weight.shape[1]
+            and x.shape[1] % 128 == 0 and n % 16 == 0 and (not swiglu or weight.shape[0] % 2 == 0))
+
+
+def _weight16(weight: torch.Tensor) -> torch.Tensor:
+    if weight.stride(1) != 1 or weight.stride(0) % 8 or weight.data_ptr() % 16:
+        return weight.contiguous()
+    return weight
+
+
+def linear_rows(x: torch.Tensor, weight: torch.Tensor, swiglu: bool = False) -> torch.Tensor:
+    """``x @ weight.T`` in bf16 for decode batches (``F.linear`` without bias);
+    ``swiglu=True``: ``weight`` is the packed ``[gate; up]`` gate_up weight and
+    the result is ``silu(x @ gate.T) * (x @ up.T)`` with the rounding points of
+    the bf16 GEMM followed by ``silu_mul``."""
+    if not linear_rows_ok(x, weight, swiglu):
+        raise ValueError(f"linear_rows: unsupported x {tuple(x.shape)} / weight "
+                         f"{tuple(weight.shape)} (bf16, <= {LINEAR_ROWS_MAX} rows, K % 128)")
+    x2 = _rows2d("x", x)
+    w = _weight16(weight)
+    m, k = x2.shape
+    n = w.shape[0] // 2 if swiglu else w.shape[0]
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=x2.device)
+    check(lib().qmi_linear_rows(x2.data_ptr(), x2.stride(0), w.data_ptr(), w.stride(0), m, n, k,
+                                1 if swiglu else 0, y.data_ptr(), y.stride(0),
+                                stream_handle(x2.device)),
+          "linear_rows")
+    return y
+
+
+def linear_rows_parts(x: torch.Tensor, weight: torch.Tensor) -> RowParts:
+    """``x @ weight.T`` as fp32 split-K partial products (see ``RowParts``)."""
+    if not linear_rows_ok(x, weight):
+        raise ValueError(f"linear_rows_parts: unsupported x {tuple(x.shape)} / weight "
+                         f"{tuple(weight.shape)}")
+    x2 = _rows2d("x", x)
+    w = _weight16(weight)
+    m, k = x2.shape
+    n = w.shape[0]
+    L = lib()
+    n_parts = L.qmi_linear_rows_parts_count(m, n, k)
+    if n_parts <= 0:
+        raise ValueError("linear_rows_parts: unsupported shape")
+    parts = torch.empty((n_parts, m, n), dtype=torch.float32, device=x2.device)
+    check(L.qmi_linear_rows_parts(x2.data_ptr(), x2.stride(0), w.data_ptr(), w.stride(0), m, n, k,
+                                  parts.data_ptr(), n_parts, stream_handle(x2.device)),
+          "linear_rows_parts")
+    return RowParts(parts)
+
+
+def add_rms_norm_parts(x: RowParts, residual: torch.Tensor, weight: torch.Tensor, eps: float):
+    """``add_rms_norm`` with ``x`` given as partial products: ``s = bf16(sum
+    parts) + residual``; returns ``(rms_norm(s), bf16(s))``."""
+    parts = x.parts
+    r2 = _rows2d("residual", residual)
+    if parts.dim() != 3 or tuple(parts.shape[1:]) != tuple(r2.shape) or not parts.is_contiguous():
+        raise ValueError("parts must be a contiguous [S, M, N] tensor matching residual [M, N]")
+    w = weight.to(torch.bfloat16).contiguous()
+    y = torch.empty(r2.shape, dtype=torch.bfloat16, device=r2.device)
+    r_out = torch.empty_like(y)
+    check(lib().qmi_add_rms_norm_parts(parts.data_ptr(), parts.shape[0], r2.shape[0], r2.data_ptr(),
+                                       r2.stride(0), r_out.data_ptr(), r_out.stride(0), w.data_ptr(),
+                                       y.data_ptr(), y.stride(0), r2.shape[1], float(eps),
+                                       stream_handle(r2.device)),
+          "add_rms_norm_parts")
+    return y.view(residual.shape), r_out.view(residual.shape)
+
+
+# ---------------------------------------------------------------------------
 # Log-softmax gather (qwen3_grpo_train.py:46-53)
 # ---------------------------------------------------------------------------
 def _rows_view(logits: torch.Tensor, ids: torch.Tensor):

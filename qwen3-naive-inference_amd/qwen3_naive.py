@@ -77,6 +77,16 @@ def _use_kernels(*tensors: torch.Tensor) -> bool:
     return all(t.is_cuda for t in tensors)
 
 
+def _decode_linear(proj: nn.Linear, x: torch.Tensor, parts: bool = False):
+    """A decode-step projection: the HIP decode-batch GEMM for bf16 inference
+    at <= 256 rows (as fp32 partial products when ``parts``: the residual add
+    + RMSNorm that follows sums them), else ``proj(x)``."""
+    w = proj.weight
+    if proj.bias is None and _use_kernels(x, w) and K.linear_rows_ok(x, w):
+        return K.linear_rows_parts(x, w) if parts else K.linear_rows(x, w)
+    return proj(x)
+
+
 class RMSNorm(nn.Module):
     """RMSNorm with optional fused residual add (qwen3_naive.py:150-175)."""
 
@@ -94,6 +104,11 @@ class RMSNorm(nn.Module):
         return y if residual is None else (y, res)
 
     def forward(self, x, residual=None):
+        if isinstance(x, K.RowParts):  # a decode projection's split-K partial products
+            if residual is None:
+                x = x.dense()
+            else:
+                return K.add_rms_norm_parts(x, residual, self.weight, self.eps)
         if x.dtype != torch.bfloat16 or not _use_kernels(x, self.weight):
             return self._torch(x, residual)
         if residual is None:
@@ -180,10 +195,10 @@ class Qwen3Attention(nn.Module):
         v = qkv[:, self.q_size + self.kv_size:].view(x.shape[0], self.num_kv_heads, self.head_dim)
         return q, k, v
 
-    def _project_store(self, x, positions, slots):
+    def _project_store(self, x, positions, slots, decode=False):
         """qkv projection + fused QK-norm/RoPE/KV-store kernel -> q [N,Hq,D]; the
         rotated k and v land in the cache rows ``slots``."""
-        qkv = self.qkv_proj(x)
+        qkv = _decode_linear(self.qkv_proj, x) if decode else self.qkv_proj(x)
         return K.qk_norm_rope_store(qkv, self.q_norm.weight, self.k_norm.weight, positions,
                                     self._cos_sin(x.device), self.num_heads, self.num_kv_heads,
                                     self.eps, self.k_cache, self.v_cache, slots)
@@ -233,11 +248,11 @@ class Qwen3Attention(nn.Module):
             ctx = context_lens.long()
             blk = block_tables.long().gather(1, (ctx // BLOCK_SIZE)[:, None])[:, 0]
             slot_mapping = (blk * BLOCK_SIZE + ctx % BLOCK_SIZE).to(torch.int32)
-        q = self._project_store(x, positions, slot_mapping)
+        q = self._project_store(x, positions, slot_mapping, decode=True)
         o = K.paged_decode_attention(q, self.k_cache, self.v_cache, context_lens, block_tables,
                                      self.scale, seqlen_bias=1,
                                      pages_per_split=self.decode_pages_per_split)
-        return self.o_proj(o.view(batch, -1))
+        return _decode_linear(self.o_proj, o.view(batch, -1), parts=True)
 
 
 class Qwen3MLP(nn.Module):
@@ -254,6 +269,16 @@ class Qwen3MLP(nn.Module):
             return self.down_proj(K.silu_mul(gu))
         gate, up = gu.chunk(2, dim=-1)
         return self.down_proj(F.silu(gate) * up)
+
+    def forward_decode(self, x):
+        """Decode step: gate_up GEMM with the SwiGLU epilogue, then down_proj as
+        partial products for the next residual add + RMSNorm (HIP decode-batch
+        GEMMs at <= 256 rows; otherwise as ``forward``)."""
+        w = self.gate_up_proj.weight
+        if (self.gate_up_proj.bias is None and _use_kernels(x, w)
+                and K.linear_rows_ok(x, w, swiglu=True)):
+            return _decode_linear(self.down_proj, K.linear_rows(x, w, swiglu=True), parts=True)
+        return self.forward(x)
 
 
 class Qwen3DecoderLayer(nn.Module):
@@ -287,7 +312,7 @@ class Qwen3DecoderLayer(nn.Module):
             h, residual = self.input_layernorm(x, residual)
         h = self.self_attn.forward_decode(h, positions, context_lens, block_tables, slot_mapping)
         h, residual = self.post_attention_layernorm(h, residual)
-        return self.mlp(h), residual
+        return self.mlp.forward_decode(h), residual
 
 
 class Qwen3Model(nn.Module):

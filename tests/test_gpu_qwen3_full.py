@@ -107,13 +107,17 @@ def test_config3_full_decode_step(pkg, qwen3):
         layer_io = {}
         with torch.no_grad():
             hcur, res = m.model.embed_tokens(ids), None
+            # A layer hands the next its MLP output as split-K partial products
+            # (K.RowParts); dense() is that projection's bf16 output.
+            dense = lambda t: t.dense() if isinstance(t, pkg.kernels.RowParts) else t  # noqa: E731
             for li, layer in enumerate(m.model.layers):
                 if li in CHECK_LAYERS:
-                    d_in = None if res is None else hcur[rows].float().cpu()
+                    d_in = None if res is None else dense(hcur)[rows].float().cpu()
                     r_in = (hcur if res is None else res)[rows].float().cpu()
                 hcur, res = layer.forward_decode(hcur, pos, ctx, bt, slots, res)
                 if li in CHECK_LAYERS:
-                    layer_io[li] = (d_in, r_in, hcur[rows].float().cpu(), res[rows].float().cpu())
+                    layer_io[li] = (d_in, r_in, dense(hcur)[rows].float().cpu(),
+                                    res[rows].float().cpu())
             h, _ = m.model.norm(hcur, res)
             h = h.clone()
             logits = m.lm_head(h).float()
