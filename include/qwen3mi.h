@@ -300,7 +300,8 @@ int qmi_linear_rows_parts(const uint16_t* x, int64_t x_stride, const uint16_t* w
  * qmi_add_rms_norm: s = x + residual (fp32), residual_out = bf16(s),
  * y = bf16(s * rsqrt(mean(s^2) + eps) * w).  Replaces the o_proj / down_proj
  * output feeding RMSNorm._add_rms_norm (qwen3_naive.py:163-169).
- * parts [n_parts][m][n] fp32 contiguous; n % 8 == 0, n <= 4096; rows and the
+ * parts [n_parts][m][n] fp32 contiguous, n_parts in {1, 2, 4, 8} (the counts
+ * qmi_linear_rows_parts_count returns); n % 8 == 0, n <= 4096; rows and the
  * weight 16-byte aligned with strides % 8 == 0.
  */
 int qmi_add_rms_norm_parts(const float* parts, int64_t n_parts, int64_t m,

@@ -187,8 +187,9 @@ __global__ __launch_bounds__(kThreads) void linear_rows_kernel(
 constexpr int kNormThreads = 128;
 constexpr int kNormVec = 4;  // 8-element chunks per lane: n <= 4096
 
+template <int S>
 __global__ __launch_bounds__(kNormThreads) void add_rms_norm_parts_kernel(
-    const float* __restrict__ part, int S, int64_t M, const uint16_t* __restrict__ res_in,
+    const float* __restrict__ part, int64_t M, const uint16_t* __restrict__ res_in,
     int64_t res_in_stride, uint16_t* __restrict__ res_out, int64_t res_out_stride,
     const uint16_t* __restrict__ wgt, uint16_t* __restrict__ y, int64_t y_stride, int n,
     float eps) {
@@ -205,11 +206,19 @@ __global__ __launch_bounds__(kNormThreads) void add_rms_norm_parts_kernel(
     if (c < nvec) {
       wv[k] = load_u4(wgt + 8 * c);
       const float* p = part + row * n + 8 * c;
-      f32x4_t a0 = *reinterpret_cast<const f32x4_t*>(p);
-      f32x4_t a1 = *reinterpret_cast<const f32x4_t*>(p + 4);
+      // All parts' loads go out together (S is a compile-time count), then
+      // they are summed in part order.
+      f32x4_t pa[S], pb[S];
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        pa[s] = *reinterpret_cast<const f32x4_t*>(p + (int64_t)s * M * n);
+        pb[s] = *reinterpret_cast<const f32x4_t*>(p + (int64_t)s * M * n + 4);
+      }
+      f32x4_t a0 = pa[0], a1 = pb[0];
+#pragma unroll
       for (int s = 1; s < S; ++s) {
-        a0 += *reinterpret_cast<const f32x4_t*>(p + (int64_t)s * M * n);
-        a1 += *reinterpret_cast<const f32x4_t*>(p + (int64_t)s * M * n + 4);
+        a0 += pa[s];
+        a1 += pb[s];
       }
       const uint4 r = load_u4(res_in + row * res_in_stride + 8 * c);
       const uint32_t rw[4] = {r.x, r.y, r.z, r.w};
@@ -271,9 +280,10 @@ Cfg pick(int64_t m, int64_t n, int64_t k, int epi) {
     c.nt = 64;
     c.ns = 3;
   }
-  if (epi == kParts) {
+  if (epi == kParts) {  // 1, 2, 4 or 8 parts (the summing norm is specialised for those)
     const int64_t tiles = n_mt * (n / c.nt);
-    c.s = (int)std::max<int64_t>(1, std::min<int64_t>({256 / tiles, 8, k / kKC}));
+    const int64_t want = std::max<int64_t>(1, std::min<int64_t>({256 / tiles, 8, k / kKC}));
+    c.s = want >= 8 ? 8 : want >= 4 ? 4 : want >= 2 ? 2 : 1;
   }
   return c;
 }
@@ -364,14 +374,25 @@ extern "C" int qmi_add_rms_norm_parts(const float* parts, int64_t n_parts, int64
   if (m < 0 || n <= 0 || n_parts <= 0) return QMI_E_BAD_SHAPE;
   if (m == 0) return QMI_OK;
   if (!parts || !residual || !residual_out || !weight || !y) return QMI_E_NULL_POINTER;
-  if (n % 8 || n > 8 * kNormThreads * kNormVec || m > 0x7fffffffLL || n_parts > 64)
+  if (n % 8 || n > 8 * kNormThreads * kNormVec || m > 0x7fffffffLL ||
+      (n_parts != 1 && n_parts != 2 && n_parts != 4 && n_parts != 8))
     return QMI_E_UNSUPPORTED;
   if (residual_stride % 8 || residual_out_stride % 8 || y_stride % 8 || !al16(parts) ||
       !al16(residual) || !al16(residual_out) || !al16(y) || !al16(weight))
     return QMI_E_BAD_STRIDE;
-  hipLaunchKernelGGL(add_rms_norm_parts_kernel, dim3((unsigned)m), dim3(kNormThreads), 0,
-                     reinterpret_cast<hipStream_t>(stream), parts, (int)n_parts, m, residual,
-                     residual_stride, residual_out, residual_out_stride, weight, y, y_stride,
-                     (int)n, eps);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+#define QMI_NP(SS)                                                                             \
+  case SS:                                                                                     \
+    hipLaunchKernelGGL(add_rms_norm_parts_kernel<SS>, dim3((unsigned)m), dim3(kNormThreads), 0, \
+                       st, parts, m, residual, residual_stride, residual_out,                   \
+                       residual_out_stride, weight, y, y_stride, (int)n, eps);                  \
+    break;
+  switch (n_parts) {
+    QMI_NP(1)
+    QMI_NP(2)
+    QMI_NP(4)
+    QMI_NP(8)
+  }
+#undef QMI_NP
   QMI_RETURN_LAUNCH_STATUS();
 }
