@@ -25,7 +25,7 @@
 //     rows and writes silu(bf16(g)) * bf16(u) rounded once (the rounding
 //     points of a bf16 GEMM followed by silu_mul); fp32 split-K partials
 //     part[s][M][N] for the narrow projections (o_proj, down: N = hidden), so
-//     that 64 rows still give ~256 workgroups — the residual add + RMSNorm
+//     that a few rows still give ~256 workgroups — the residual add + RMSNorm
 //     that follows sums them (qmi_add_rms_norm_parts) instead of a separate
 //     reduction.
 #include <algorithm>
@@ -263,9 +263,12 @@ __global__ __launch_bounds__(kNormThreads) void add_rms_norm_parts_kernel(
 inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline bool al8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
 
-// Tile choice (measured on the Qwen3-0.6B shapes at 64 and 256 rows): 16
-// weight rows per tile unless that gives 1,024+ workgroups (then 64); SwiGLU
-// 32 (16 gate + 16 up); the split of K fills ~256 workgroups.
+// Tile choice, by the number of 64-row tiles (measured on the Qwen3-0.6B
+// shapes in HIP graphs of 28 layers): one row tile — 16 weight rows per tile
+// (32 for SwiGLU: 16 gate + 16 up), which alone gives ~256 workgroups; two —
+// 32 (64); more — 64 weight rows, so that the activations are re-read
+// through L2 by fewer column tiles.  The K split of the partial products
+// fills ~256 workgroups (1, 2, 4 or 8 parts).
 struct Cfg {
   int nt, ns, s;
 };
@@ -274,13 +277,14 @@ Cfg pick(int64_t m, int64_t n, int64_t k, int epi) {
   const int64_t n_mt = (m + 63) / 64;
   Cfg c{16, 4, 1};
   if (epi == kSwiGLU) {
-    c.nt = 32;
-    c.ns = m <= 64 ? 4 : 3;
-  } else if (n_mt * (n / 16) >= 1024 && n % 64 == 0) {
-    c.nt = 64;
-    c.ns = 3;
-  }
-  if (epi == kParts) {  // 1, 2, 4 or 8 parts (the summing norm is specialised for those)
+    c = n_mt == 1 ? Cfg{32, 3, 1} : n_mt == 2 ? Cfg{64, 3, 1} : Cfg{64, 2, 1};
+    if (n % (c.nt / 2)) c = Cfg{32, 3, 1};
+  } else if (epi == kPlain) {
+    c = n_mt == 1 ? Cfg{16, 4, 1} : n_mt == 2 ? Cfg{32, 3, 1} : Cfg{64, 3, 1};
+    if (n % c.nt) c = Cfg{16, 4, 1};
+  } else {
+    c = n_mt <= 2 ? Cfg{16, 4, 1} : Cfg{64, 2, 1};
+    if (n % c.nt) c = Cfg{16, 4, 1};
     const int64_t tiles = n_mt * (n / c.nt);
     const int64_t want = std::max<int64_t>(1, std::min<int64_t>({256 / tiles, 8, k / kKC}));
     c.s = want >= 8 ? 8 : want >= 4 ? 4 : want >= 2 ? 2 : 1;
@@ -315,11 +319,16 @@ int launch(const uint16_t* x, int64_t x_stride, const uint16_t* w, int64_t w_str
     return QMI_OK;                                                                                \
   }
   if constexpr (EPI == kSwiGLU) {
-    QMI_LR(32, 4)
     QMI_LR(32, 3)
+    QMI_LR(64, 3)
+    QMI_LR(64, 2)
+  } else if constexpr (EPI == kPlain) {
+    QMI_LR(16, 4)
+    QMI_LR(32, 3)
+    QMI_LR(64, 3)
   } else {
     QMI_LR(16, 4)
-    QMI_LR(64, 3)
+    QMI_LR(64, 2)
   }
 #undef QMI_LR
   return QMI_E_UNSUPPORTED;

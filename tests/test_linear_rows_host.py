@@ -9,8 +9,11 @@ def test_parts_count(pkg):
     # 64 rows: 64 column tiles of 16 -> split K in 4 (256 workgroups).
     assert L.qmi_linear_rows_parts_count(64, 1024, 2048) == 4
     assert L.qmi_linear_rows_parts_count(64, 1024, 3072) == 4
-    # 256 rows already give 256 tiles: no split.
-    assert L.qmi_linear_rows_parts_count(256, 1024, 2048) == 1
+    # 128 rows: 128 tiles of 16 columns -> 2 parts; 256 rows: tiles of 64
+    # weight rows (fewer re-reads of the activations) -> 64 tiles, 4 parts.
+    assert L.qmi_linear_rows_parts_count(128, 1024, 2048) == 2
+    assert L.qmi_linear_rows_parts_count(256, 1024, 2048) == 4
+    assert L.qmi_linear_rows_parts_count(256, 1024, 3072) == 4
     # Never more parts than 128-element K chunks.
     assert L.qmi_linear_rows_parts_count(1, 16, 128) == 1
     assert L.qmi_linear_rows_parts_count(1, 16, 256) == 2
