@@ -740,20 +740,63 @@ void varlen_prefill_kernel(
     }
 
     // ---- normalise and write O[query][dims] ----
+    // Staged through LDS (the K buffers are idle after the last tile's
+    // barrier), so that the stores run along token rows: a lane's
+    // accumulators hold 8-byte pieces of 16 query rows, which stored directly
+    // would be 16 separate 32-byte pieces per store.  Staging row = query of
+    // the block * G + head of the group; 16-byte chunk c of the row sits at
+    // c ^ (query % 16), so the writes of a 16-lane group (16 queries) and the
+    // row reads are free of bank conflicts.  With contiguous heads
+    // (head stride 128) the G heads of a token are G x 256 contiguous bytes
+    // and each lane stores 16 bytes; other strides store 8-byte halves.
+    {
+      uint16_t* stage = &sK[0][0];
+      const int hg = wave / kWavesPerHead;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const float inv = l_tot[j] > 0.f ? 1.0f / l_tot[j] : 0.f;
-      const int my_q = wq0 + 16 * j + l16;
-      if (my_q < Lq) {
-        uint16_t* orow =
-            out + (int64_t)(q_start + my_q) * out_tok_stride + (int64_t)qh * out_head_stride;
+      for (int j = 0; j < 2; ++j) {
+        const float inv = l_tot[j] > 0.f ? 1.0f / l_tot[j] : 0.f;
+        const int qi = (wave % kWavesPerHead) * kWaveQ + 16 * j + l16;  // qi % 16 == l16
+        uint16_t* srow = stage + (qi * G + hg) * kHeadDim;
 #pragma unroll
         for (int db = 0; db < 8; ++db) {
           const uint32_t w0 = pack_bf16x2(acc_o[j][db][0] * inv, acc_o[j][db][1] * inv);
           const uint32_t w1 = pack_bf16x2(acc_o[j][db][2] * inv, acc_o[j][db][3] * inv);
-          *reinterpret_cast<uint2*>(orow + db * 16 + 4 * g4) = make_uint2(w0, w1);
+          const int c16 = 2 * db + (g4 >> 1);  // chunk of dims 16 db + 4 g4 .. +3
+          *reinterpret_cast<uint2*>(srow + 8 * (c16 ^ l16) + 4 * (g4 & 1)) = make_uint2(w0, w1);
         }
       }
+      __syncthreads();
+      // 16-byte chunks of the block's O: kQB x G x 256 bytes = 2048 chunks
+      // for every G; thread t stores chunks t, t + 256, ...
+      constexpr int kChunks = kQB * G * kHeadDim / 8;
+      static_assert(kChunks % kThreads == 0, "output chunks per thread");
+      const bool wide = out_head_stride == kHeadDim && out_tok_stride % 8 == 0 &&
+                        (reinterpret_cast<uintptr_t>(out) & 15u) == 0;  // uniform
+      const int rows_valid = min(kQB, Lq - q0);
+      uint16_t* obase = out + (int64_t)(q_start + q0) * out_tok_stride + (int64_t)kvh * G * out_head_stride;
+      // Opaque copy of the thread index: keeps the chunk addresses from being
+      // hoisted out of the item loop (they would stay live across the tile
+      // loop and push it over the register budget).
+      int t_ep = tid;
+      asm volatile("" : "+v"(t_ep));
+#pragma unroll
+      for (int i = 0; i < kChunks / kThreads; ++i) {
+        const int id = i * kThreads + t_ep;
+        const int tok = id / (G * 16), hgr = (id / 16) % G, c16 = id % 16;
+        if (tok < rows_valid) {
+          const uint4 v =
+              *reinterpret_cast<const uint4*>(stage + (tok * G + hgr) * kHeadDim + 8 * (c16 ^ (tok & 15)));
+          uint16_t* dst = obase + (int64_t)tok * out_tok_stride + (int64_t)hgr * out_head_stride + 8 * c16;
+          if (wide) {
+            *reinterpret_cast<uint4*>(dst) = v;
+          } else {
+            *reinterpret_cast<uint2*>(dst) = make_uint2(v.x, v.y);
+            *reinterpret_cast<uint2*>(dst + 4) = make_uint2(v.z, v.w);
+          }
+        }
+      }
+      // The next item's first tile overwrites the staging rows only after
+      // advance()'s barrier.
     }
     advance();
   }  // item loop

@@ -411,3 +411,40 @@ def test_prefill_queue_modes(pkg, gpu, lens_q, prefix, hq, hkv):
     torch.cuda.synchronize()
     assert st == 0
     assert (out1.float() - whole.float()).abs().max().item() <= 1e-2
+
+
+@pytest.mark.parametrize("layout", ["head_stride_136", "offset_8_bytes"])
+def test_prefill_strided_out_view(pkg, gpu, layout):
+    """O written into a view of a larger buffer: rows staged in LDS are stored
+    as 8-byte halves when the heads are not contiguous or the view is not
+    16-byte aligned; nothing outside the view is touched."""
+    lens_q, prefix = [300, 64, 200], 300
+    lens_k = [prefix + n for n in lens_q]
+    kc, vc, bt = _pool(91, lens_k)
+    tq = sum(lens_q)
+    g = torch.Generator().manual_seed(92)
+    q = torch.randn(tq, 16, 128, generator=g).to(torch.bfloat16)
+    cu_q = [0]
+    for n in lens_q:
+        cu_q.append(cu_q[-1] + n)
+    cu_k = [0]
+    for n in lens_k:
+        cu_k.append(cu_k[-1] + n)
+    if layout == "head_stride_136":
+        big = torch.zeros(tq, 16, 136, dtype=torch.bfloat16, device=gpu)
+        out = big[:, :, 4:132]
+    else:
+        big = torch.zeros(tq * 16 * 128 + 8, dtype=torch.bfloat16, device=gpu)
+        out = big[4:4 + tq * 16 * 128].view(tq, 16, 128)
+    print(f"[prefill] strided out {layout}", flush=True)
+    res = pkg.kernels.varlen_prefill_attention(
+        q.to(gpu), kc.to(gpu), vc.to(gpu), torch.tensor(cu_q, dtype=torch.int32, device=gpu),
+        torch.tensor(cu_k, dtype=torch.int32, device=gpu), max(lens_q), max(lens_k), SCALE, True,
+        bt.to(gpu), out)
+    torch.cuda.synchronize()
+    assert res.data_ptr() == out.data_ptr()
+    _check(out, q, kc, vc, cu_q, cu_k, bt)
+    if layout == "head_stride_136":
+        assert not big[:, :, :4].any() and not big[:, :, 132:].any()
+    else:
+        assert not big[:4].any() and not big[4 + tq * 16 * 128:].any()
