@@ -282,28 +282,6 @@ int qmi_linear_rows(const uint16_t* x, int64_t x_stride, const uint16_t* w, int6
                     int64_t y_stride, void* stream);
 
 /*
- * The decode step's qkv projection with its per-head QK-RMSNorm, RoPE and KV
- * store as the GEMM's epilogue: qmi_linear_rows(x, w) followed by
- * qmi_qk_norm_rope_store in one launch, the qkv activation never written.
- * Replaces qkv_proj -> q_norm / k_norm -> rotary_emb -> store_kvcache of
- * Qwen3Attention.forward_decode (qwen3_naive.py:654-668).  w is the packed
- * [(num_q_heads + 2 num_kv_heads) * 128, k] qkv weight (q, k, v heads);
- * x [m, k]; same rules as qmi_linear_rows for x and w (m <= 256, k % 128 ==
- * 0).  Outputs as qmi_qk_norm_rope_store: q_out [m, q_stride] (8-byte
- * aligned, q_stride % 4 == 0), rotated k and v rows at cache slot
- * slot_mapping[i] (slots outside [0, n_slots) skipped); head_dim == 128.
- * Results equal the two-call form up to the fp32 order of each head's sum
- * of squares (v rows bit-identical).
- */
-int qmi_linear_rows_qk_norm_rope_store(
-    const uint16_t* x, int64_t x_stride, const uint16_t* w, int64_t w_stride, int64_t m,
-    int64_t k, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
-    const uint16_t* q_norm_weight, const uint16_t* k_norm_weight, const int64_t* positions,
-    const float* cos_sin_cache, int64_t max_position, uint16_t* q_out, int64_t q_stride,
-    uint16_t* k_cache, uint16_t* v_cache, const int32_t* slot_mapping, int64_t n_slots, float eps,
-    void* stream);
-
-/*
  * Split-K form of qmi_linear_rows for the narrow projections that feed a
  * residual add + RMSNorm (o_proj, qwen3_naive.py:428, :683; down_proj,
  * :693, :702): writes parts[s][m][n] fp32 (contiguous) with

@@ -69,9 +69,6 @@ SIGNATURES: dict[str, tuple] = {
     "qmi_silu_mul": (ctypes.c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p]),
     "qmi_linear_rows": (ctypes.c_int, [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32,
                                        _c_p, _c_i64, _c_p]),
-    "qmi_linear_rows_qk_norm_rope_store": (ctypes.c_int, [
-        _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p,
-        _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_f32, _c_p]),
     "qmi_linear_rows_parts_count": (_c_i64, [_c_i64, _c_i64, _c_i64]),
     "qmi_linear_rows_parts": (ctypes.c_int, [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
                                              _c_p, _c_i64, _c_p]),

@@ -27,18 +27,10 @@
 //     part[s][M][N] for the narrow projections (o_proj, down: N = hidden), so
 //     that a few rows still give ~256 workgroups — the residual add + RMSNorm
 //     that follows sums them (qmi_add_rms_norm_parts) instead of a separate
-//     reduction; and, for qkv_proj, the per-head QK-RMSNorm + RoPE + KV store
-//     of the decode step (qwen3_naive.py:661-668): a tile is one 128-column
-//     head, so a lane holds the RoPE partners c and c + 64 and a row's sum of
-//     squares is a 4-lane reduction; q heads go to q_out, k and v heads
-//     straight to their cache slots (the qkv activation never reaches HBM).
+//     reduction.
 #include <algorithm>
 
 #include "qmi_common.h"
-
-#ifndef QMI_QKROPE_STAGES
-#define QMI_QKROPE_STAGES 3
-#endif
 
 namespace {
 
@@ -62,31 +54,14 @@ __device__ __forceinline__ u4v_t ds_read16(uint32_t addr) {
   return r;
 }
 
-enum Epi { kPlain = 0, kSwiGLU = 1, kParts = 2, kQkRope = 3 };
-
-// Epilogue inputs of kQkRope (the per-head QK-norm + RoPE + KV store).
-struct QkArgs {
-  const uint16_t* q_w;      // q_norm weight [128]
-  const uint16_t* k_w;      // k_norm weight [128]
-  const int64_t* positions;  // [M]
-  const float* cos_sin;     // [max_pos, 128]: cos(p f_i) at i, sin(p f_i) at 64 + i
-  int64_t max_pos;
-  uint16_t* q_out;          // [M, q_stride] rows of n_q_heads * 128
-  int64_t q_stride;
-  uint16_t* k_cache;        // [n_slots, n_kv_heads, 128]
-  uint16_t* v_cache;
-  const int32_t* slots;     // [M]; outside [0, n_slots) skips the store
-  int64_t n_slots;
-  int n_q_heads, n_kv_heads;
-  float eps;
-};
+enum Epi { kPlain = 0, kSwiGLU = 1, kParts = 2 };
 
 // NT: weight rows per tile (output columns; NT / 2 for SwiGLU).
 template <int NT, int NSTAGE, int EPI>
 __global__ __launch_bounds__(kThreads) void linear_rows_kernel(
     const uint16_t* __restrict__ x, int64_t x_stride, const uint16_t* __restrict__ w,
     int64_t w_stride, uint16_t* __restrict__ y, int64_t y_stride, float* __restrict__ part,
-    int M, int N, int K, int S, QkArgs qa) {
+    int M, int N, int K, int S) {
   constexpr int XB = 64 * kRowB, WB = NT * kRowB, SB = XB + WB;
   constexpr int WPW = NT / 16;  // weight wave-loads (4 rows each) per wave per chunk
   constexpr int LPW = 4 + WPW;  // loads per wave per chunk
@@ -144,28 +119,6 @@ __global__ __launch_bounds__(kThreads) void linear_rows_kernel(
   for (int b = 0; b < NB; ++b) acc[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int st = 0; st < NSTAGE - 1; ++st) issue(kc0 + min(st, nk - 1), st);
-  // kQkRope: the epilogue's inputs are loaded once the ring's first chunks are
-  // on their way (the position -> cos / sin pair is the only dependent load).
-  [[maybe_unused]] int32_t e_slot = -1;
-  [[maybe_unused]] f32x4_t e_cs[8];
-  [[maybe_unused]] uint2 e_nw[8];
-  if constexpr (EPI == kQkRope) {
-    const int erow = min(m0 + 16 * wave + l16, M - 1);
-    e_slot = qa.slots[erow];
-    if (nt < qa.n_q_heads + qa.n_kv_heads) {
-      const uint16_t* nw = nt < qa.n_q_heads ? qa.q_w : qa.k_w;
-#pragma unroll
-      for (int b = 0; b < 8; ++b) e_nw[b] = *reinterpret_cast<const uint2*>(nw + 16 * b + 4 * g4);
-      int64_t pos = qa.positions[erow];
-      pos = pos < 0 ? 0 : (pos >= qa.max_pos ? qa.max_pos - 1 : pos);
-      const float* cs = qa.cos_sin + pos * 128;
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        e_cs[b] = *reinterpret_cast<const f32x4_t*>(cs + 16 * b + 4 * g4);
-        e_cs[b + 4] = *reinterpret_cast<const f32x4_t*>(cs + 64 + 16 * b + 4 * g4);
-      }
-    }
-  }
   for (int k = 0; k < nk; ++k) {
     const int st = k % NSTAGE;
     // Chunk k has landed once at most the later NSTAGE - 2 chunks' loads are
@@ -185,13 +138,9 @@ __global__ __launch_bounds__(kThreads) void linear_rows_kernel(
         asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(bv[0]) :: "memory");
       else if constexpr (NB == 2)
         asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(bv[0]), "+v"(bv[1]) :: "memory");
-      else if constexpr (NB == 4)
-        asm volatile("s_waitcnt lgkmcnt(0)"
-                     : "+v"(a), "+v"(bv[0]), "+v"(bv[1]), "+v"(bv[2]), "+v"(bv[3]) :: "memory");
       else
         asm volatile("s_waitcnt lgkmcnt(0)"
-                     : "+v"(a), "+v"(bv[0]), "+v"(bv[1]), "+v"(bv[2]), "+v"(bv[3]), "+v"(bv[4]),
-                       "+v"(bv[5]), "+v"(bv[6]), "+v"(bv[7]) :: "memory");
+                     : "+v"(a), "+v"(bv[0]), "+v"(bv[1]), "+v"(bv[2]), "+v"(bv[3]) :: "memory");
 #pragma unroll
       for (int b = 0; b < NB; ++b)
         acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, bv[b]),
@@ -224,74 +173,11 @@ __global__ __launch_bounds__(kThreads) void linear_rows_kernel(
       *reinterpret_cast<uint2*>(y + (int64_t)row * y_stride + col) =
           make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
     }
-  } else if constexpr (EPI == kParts) {
+  } else {
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       const int col = n0 + 16 * b + 4 * g4;
       *reinterpret_cast<f32x4_t*>(part + ((int64_t)s * M + row) * N + col) = acc[b];
-    }
-  } else {
-    static_assert(NT == 128, "kQkRope: one 128-column head per tile");
-    typedef __attribute__((ext_vector_type(2))) unsigned int u32x2_t;
-    // Lane (l16, g4) holds head columns 16 b + 4 g4 + r (b < 8, r < 4) of row
-    // `row`: the projection's bf16 output first (the reference's qkv tensor).
-    float xv[8][4];
-#pragma unroll
-    for (int b = 0; b < 8; ++b)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) xv[b][r] = bf16_to_f32(f32_to_bf16(acc[b][r]));
-    const int hq = qa.n_q_heads, hk = qa.n_kv_heads;
-    const bool slot_ok = e_slot >= 0 && e_slot < qa.n_slots;
-    if (nt >= hq + hk) {  // v head: only its cache row
-      if (slot_ok) {
-        uint16_t* dst = qa.v_cache + ((int64_t)e_slot * hk + (nt - hq - hk)) * 128 + 4 * g4;
-#pragma unroll
-        for (int b = 0; b < 8; ++b)
-          __builtin_nontemporal_store(
-              u32x2_t{pack_bf16x2(xv[b][0], xv[b][1]), pack_bf16x2(xv[b][2], xv[b][3])},
-              reinterpret_cast<u32x2_t*>(dst + 16 * b));
-      }
-      return;
-    }
-    float ss = 0.f;
-#pragma unroll
-    for (int b = 0; b < 8; ++b)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) ss += xv[b][r] * xv[b][r];
-    ss = rows4_sum(ss);  // the row's four lanes l16 + 16 g4
-    const float inv = rsqrtf(ss / 128.f + qa.eps);
-    float nv[8][4];
-#pragma unroll
-    for (int b = 0; b < 8; ++b) {
-      const float wq[4] = {bf16_lo(e_nw[b].x), bf16_hi(e_nw[b].x), bf16_lo(e_nw[b].y),
-                           bf16_hi(e_nw[b].y)};
-      // QK-norm output is bf16 in the reference before RoPE reads it.
-#pragma unroll
-      for (int r = 0; r < 4; ++r) nv[b][r] = bf16_to_f32(f32_to_bf16(xv[b][r] * inv * wq[r]));
-    }
-    uint2 ov[8];
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      float o1[4], o2[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float c = e_cs[b][r], sn = e_cs[b + 4][r];
-        o1[r] = nv[b][r] * c - nv[b + 4][r] * sn;
-        o2[r] = nv[b + 4][r] * c + nv[b][r] * sn;
-      }
-      ov[b] = make_uint2(pack_bf16x2(o1[0], o1[1]), pack_bf16x2(o1[2], o1[3]));
-      ov[b + 4] = make_uint2(pack_bf16x2(o2[0], o2[1]), pack_bf16x2(o2[2], o2[3]));
-    }
-    if (nt < hq) {
-      uint16_t* dst = qa.q_out + (int64_t)row * qa.q_stride + nt * 128 + 4 * g4;
-#pragma unroll
-      for (int b = 0; b < 8; ++b) *reinterpret_cast<uint2*>(dst + 16 * b) = ov[b];
-    } else if (slot_ok) {
-      uint16_t* dst = qa.k_cache + ((int64_t)e_slot * hk + (nt - hq)) * 128 + 4 * g4;
-#pragma unroll
-      for (int b = 0; b < 8; ++b)
-        __builtin_nontemporal_store(u32x2_t{ov[b].x, ov[b].y},
-                                    reinterpret_cast<u32x2_t*>(dst + 16 * b));
     }
   }
 }
@@ -422,21 +308,17 @@ int check_args(const void* x, int64_t x_stride, const void* w, int64_t w_stride,
 template <int EPI>
 int launch(const uint16_t* x, int64_t x_stride, const uint16_t* w, int64_t w_stride, uint16_t* y,
            int64_t y_stride, float* part, int64_t m, int64_t n, int64_t k, const Cfg& c,
-           hipStream_t st, const QkArgs& qa = QkArgs{}) {
+           hipStream_t st) {
   const int out = EPI == kSwiGLU ? c.nt / 2 : c.nt;
   if (n % out) return QMI_E_UNSUPPORTED;
   const unsigned grid = (unsigned)(((m + 63) / 64) * (n / out) * c.s);
 #define QMI_LR(NT, NS)                                                                           \
   if (c.nt == NT && c.ns == NS) {                                                                \
     hipLaunchKernelGGL((linear_rows_kernel<NT, NS, EPI>), dim3(grid), dim3(kThreads), 0, st, x,  \
-                       x_stride, w, w_stride, y, y_stride, part, (int)m, (int)n, (int)k, c.s,    \
-                       qa);                                                                      \
+                       x_stride, w, w_stride, y, y_stride, part, (int)m, (int)n, (int)k, c.s);   \
     return QMI_OK;                                                                                \
   }
-  if constexpr (EPI == kQkRope) {
-    QMI_LR(128, 3)
-    QMI_LR(128, 2)
-  } else if constexpr (EPI == kSwiGLU) {
+  if constexpr (EPI == kSwiGLU) {
     QMI_LR(32, 3)
     QMI_LR(64, 3)
     QMI_LR(64, 2)
@@ -468,36 +350,6 @@ extern "C" int qmi_linear_rows(const uint16_t* x, int64_t x_stride, const uint16
   e = activation == kSwiGLU
           ? launch<kSwiGLU>(x, x_stride, w, w_stride, y, y_stride, nullptr, m, n, k, c, st)
           : launch<kPlain>(x, x_stride, w, w_stride, y, y_stride, nullptr, m, n, k, c, st);
-  if (e != QMI_OK) return e;
-  QMI_RETURN_LAUNCH_STATUS();
-}
-
-extern "C" int qmi_linear_rows_qk_norm_rope_store(
-    const uint16_t* x, int64_t x_stride, const uint16_t* w, int64_t w_stride, int64_t m,
-    int64_t k, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
-    const uint16_t* q_norm_weight, const uint16_t* k_norm_weight, const int64_t* positions,
-    const float* cos_sin_cache, int64_t max_position, uint16_t* q_out, int64_t q_stride,
-    uint16_t* k_cache, uint16_t* v_cache, const int32_t* slot_mapping, int64_t n_slots, float eps,
-    void* stream) {
-  if (num_q_heads <= 0 || num_kv_heads <= 0 || max_position <= 0 || n_slots < 0)
-    return QMI_E_BAD_SHAPE;
-  if (head_dim != 128 || num_q_heads > 4096 || num_kv_heads > 4096) return QMI_E_UNSUPPORTED;
-  const int64_t n = (num_q_heads + 2 * num_kv_heads) * head_dim;
-  int e = check_args(x, x_stride, w, w_stride, m, n, k);
-  if (e != QMI_OK) return e;
-  if (m == 0) return QMI_OK;
-  if (!q_norm_weight || !k_norm_weight || !positions || !cos_sin_cache || !q_out || !k_cache ||
-      !v_cache || !slot_mapping)
-    return QMI_E_NULL_POINTER;
-  if (q_stride < num_q_heads * 128 || q_stride % 4 || !al8(q_out) || !al16(cos_sin_cache) ||
-      !al8(q_norm_weight) || !al8(k_norm_weight) || !al8(k_cache) || !al8(v_cache))
-    return QMI_E_BAD_STRIDE;
-  QkArgs qa{q_norm_weight, k_norm_weight, positions, cos_sin_cache, max_position, q_out, q_stride,
-            k_cache, v_cache, slot_mapping, n_slots, (int)num_q_heads, (int)num_kv_heads, eps};
-  // Three ring stages (144 KB of LDS, one workgroup per CU).
-  const Cfg c{128, QMI_QKROPE_STAGES, 1};
-  e = launch<kQkRope>(x, x_stride, w, w_stride, nullptr, 0, nullptr, m, n, k, c,
-                      reinterpret_cast<hipStream_t>(stream), qa);
   if (e != QMI_OK) return e;
   QMI_RETURN_LAUNCH_STATUS();
 }

@@ -471,58 +471,6 @@ def linear_rows(x: torch.Tensor, weight: torch.Tensor, swiglu: bool = False) -> 
     return y
 
 
-def linear_rows_qk_norm_rope_store(x: torch.Tensor, weight: torch.Tensor,
-                                   q_norm_weight: torch.Tensor, k_norm_weight: torch.Tensor,
-                                   positions: torch.Tensor, cos_sin_cache: torch.Tensor,
-                                   num_q_heads: int, num_kv_heads: int, eps: float,
-                                   k_cache: torch.Tensor, v_cache: torch.Tensor,
-                                   slot_mapping: torch.Tensor) -> torch.Tensor:
-    """The decode step's qkv projection with the QK-norm / RoPE / KV store as
-    its epilogue: ``qk_norm_rope_store(linear_rows(x, weight), ...)`` in one
-    launch (the qkv activation is never written).  Returns ``q [M, Hq, 128]``;
-    the rotated k and the v heads go to cache rows ``slot_mapping`` (-1 skips)."""
-    n = (num_q_heads + 2 * num_kv_heads) * HEAD_DIM
-    if weight.dim() != 2 or weight.shape[0] != n:
-        raise ValueError(f"weight must be [{n}, K] (q, k, v heads of 128 rows)")
-    if not linear_rows_ok(x, weight):
-        raise ValueError(f"linear_rows_qk_norm_rope_store: unsupported x {tuple(x.shape)} / "
-                         f"weight {tuple(weight.shape)} (bf16, <= {LINEAR_ROWS_MAX} rows, K % 128)")
-    x2 = _rows2d("x", x)
-    w = _weight16(weight)
-    m, k = x2.shape
-    pos = positions.reshape(-1)
-    if pos.dtype != torch.int64:
-        pos = pos.to(torch.int64)
-    if pos.shape[0] != m:
-        raise ValueError(f"positions must have {m} entries")
-    pos = pos.contiguous()
-    cache = cos_sin_cache
-    if cache.dtype != torch.float32 or cache.dim() != 2 or cache.shape[1] != HEAD_DIM:
-        raise ValueError("cos_sin_cache must be fp32 [max_position, 128]")
-    cache = cache.contiguous()
-    for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
-        _require_cuda(name, c)
-        _require_dtype(name, c, torch.bfloat16)
-        if not c.is_contiguous() or c.shape[-2:] != (num_kv_heads, HEAD_DIM):
-            raise ValueError(f"{name} must be a contiguous [..., {num_kv_heads}, 128] bf16 pool")
-    sl = slot_mapping.reshape(-1)
-    if sl.dtype != torch.int32:
-        sl = sl.to(torch.int32)
-    if sl.shape[0] != m:
-        raise ValueError(f"slot_mapping must have {m} entries")
-    sl = sl.contiguous()
-    n_slots = k_cache.numel() // (num_kv_heads * HEAD_DIM)
-    qw = q_norm_weight.to(torch.bfloat16).contiguous()
-    kw = k_norm_weight.to(torch.bfloat16).contiguous()
-    q = torch.empty((m, num_q_heads, HEAD_DIM), dtype=torch.bfloat16, device=x2.device)
-    check(lib().qmi_linear_rows_qk_norm_rope_store(
-        x2.data_ptr(), x2.stride(0), w.data_ptr(), w.stride(0), m, k, num_q_heads, num_kv_heads,
-        HEAD_DIM, qw.data_ptr(), kw.data_ptr(), pos.data_ptr(), cache.data_ptr(), cache.shape[0],
-        q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(), sl.data_ptr(), n_slots,
-        float(eps), stream_handle(x2.device)), "linear_rows_qk_norm_rope_store")
-    return q
-
-
 def linear_rows_parts(x: torch.Tensor, weight: torch.Tensor) -> RowParts:
     """``x @ weight.T`` as fp32 split-K partial products (see ``RowParts``)."""
     if not linear_rows_ok(x, weight):
