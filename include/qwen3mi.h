@@ -107,6 +107,47 @@ int qmi_paged_decode_attention(const uint16_t* q, int64_t q_seq_stride, int64_t 
                                int64_t pages_per_split, void* stream);
 
 /*
+ * The decode step's attention with the per-head QK-RMSNorm, RoPE and KV
+ * store folded in: the same results as qmi_qk_norm_rope_store(qkv, ...)
+ * (k and v heads to cache row slot_mapping[b]) followed by
+ * qmi_paged_decode_attention(q, ..., seqlen_bias = 1) on the balanced
+ * schedule, with one launch less and no q tensor.  Replaces q_norm / k_norm
+ * -> rotary_emb -> store_kvcache -> flash_attn_with_kvcache of
+ * Qwen3Attention.forward_decode (qwen3_naive.py:661-680).
+ *
+ * qkv    : [batch, qkv_stride] bf16 rows holding num_q_heads q heads, then
+ *          num_kv_heads k heads, then num_kv_heads v heads of 128 dims
+ *          (qkv_proj's packed output); 16-byte aligned, qkv_stride % 8 == 0.
+ * q_norm_weight / k_norm_weight: bf16 [128], 16-byte aligned.
+ * positions: int64 [batch] (clamped to [0, max_position)); cos_sin_cache:
+ *          fp32 [max_position, 128] (cos at i, sin at 64 + i), 16-byte aligned.
+ * slot_mapping: int32 [batch]; the new token's rows go to cache slot
+ *          slot_mapping[b] (outside [0, num_blocks * 256): not stored).  It
+ *          must be -1 or the slot of key seqlens[b] that the table maps (the
+ *          engine's decode step); key seqlens[b] is then read from the new
+ *          rows.  Sequences with seqlens[b] < 0 store nothing.
+ * The rest as qmi_paged_decode_attention with seqlen_bias 1; pages_per_split
+ * 0 (balanced split + merge) or -1 (whole units, no merge launch); the
+ * workspace is qmi_paged_decode_workspace_bytes(.., pages_per_split = 0).
+ * Supported: head_dim 128, block_size 256, num_kv_heads in {2, 4, 8, 16},
+ * ratio in {1, 2, 4}, batch <= 1024, out 16-byte aligned, strides % 8 == 0.
+ * q and k match the two-call form up to the fp32 order of each head's sum of
+ * squares (v rows bit-identical).
+ */
+int qmi_paged_decode_attention_qkv(const uint16_t* qkv, int64_t qkv_stride, int64_t num_q_heads,
+                                   int64_t num_kv_heads, int64_t head_dim,
+                                   const uint16_t* q_norm_weight, const uint16_t* k_norm_weight,
+                                   const int64_t* positions, const float* cos_sin_cache,
+                                   int64_t max_position, float eps, uint16_t* k_cache,
+                                   uint16_t* v_cache, int64_t num_blocks, int64_t block_size,
+                                   const int32_t* slot_mapping, const int32_t* seqlens,
+                                   const int32_t* block_table, int64_t bt_stride,
+                                   int64_t bt_width, int64_t batch, float scale, uint16_t* out,
+                                   int64_t out_seq_stride, int64_t out_head_stride,
+                                   float* workspace, int64_t workspace_bytes,
+                                   int64_t pages_per_split, void* stream);
+
+/*
  * Paged GQA decode attention that allocates nothing: no counterpart in the
  * reference.  For callers that cannot allocate device memory or take a
  * workspace (code under HIP graph capture, tight serving loops, harnesses

@@ -45,6 +45,16 @@ SIGNATURES: dict[str, tuple] = {
         _c_i64, _c_f32,                  # batch, scale
         _c_p, _c_i64, _c_i64,            # out, strides
         _c_i64, _c_p]),                  # pages_per_split, stream
+    "qmi_paged_decode_attention_qkv": (ctypes.c_int, [
+        _c_p, _c_i64, _c_i64, _c_i64,    # qkv, stride, heads, kv heads
+        _c_i64, _c_p, _c_p,              # head_dim, q_norm / k_norm weights
+        _c_p, _c_p, _c_i64, _c_f32,      # positions, cos_sin_cache, max_position, eps
+        _c_p, _c_p, _c_i64, _c_i64,      # caches, num_blocks, block_size
+        _c_p, _c_p,                      # slot_mapping, seqlens
+        _c_p, _c_i64, _c_i64,            # block_table, stride, width
+        _c_i64, _c_f32,                  # batch, scale
+        _c_p, _c_i64, _c_i64,            # out, strides
+        _c_p, _c_i64, _c_i64, _c_p]),    # workspace, bytes, pages_per_split, stream
     "qmi_varlen_prefill_workspace_bytes": (_c_i64, [_c_i64] * 7),
     "qmi_varlen_prefill_attention": (ctypes.c_int, [
         _c_p, _c_i64, _c_i64,            # q, strides

@@ -40,6 +40,8 @@
 // share of a workgroup), so it needs no host knowledge of the lengths and
 // holds inside a captured graph; otherwise the balanced split runs over the
 // units.
+#include <type_traits>
+
 #include "qmi_common.h"
 
 namespace {
@@ -55,6 +57,10 @@ template <int HG> constexpr int kTokGroups = 16 / HG;
 template <int HG> constexpr int kStepTokens = kTokGroups<HG> * kTok;   // divides the page
 constexpr int kSlotStride = kHeadDim + 4;      // acc[128], m, l, pad (per q head)
 constexpr int kMaxSeqScan = 1024;              // batch limit of the in-LDS prefix scan
+
+#ifndef QMI_QKV_WAVES_PER_EU
+#define QMI_QKV_WAVES_PER_EU 3
+#endif
 
 // Workgroups that take part: the launch is sized from the block-table width,
 // before the context lengths are known, so a short total would leave most
@@ -82,9 +88,15 @@ __device__ __forceinline__ int64_t owner_of(int64_t s, int64_t total, int64_t n_
 // into LDS (exclusive; off[B] = total), and the largest count into *max_steps.
 // Each lane takes ceil(B / THREADS) consecutive sequences; lane sums are scanned
 // inside each wave with shuffles and across waves through LDS.
+//
+// With `positions` given, each lane also copies its sequences' positions,
+// clamped to [0, max_pos), into pos_out (LDS), so that a segment's RoPE row
+// needs no dependent global load.
 template <int THREADS, int TS>
 __device__ void scan_steps(const int32_t* __restrict__ seqlens, int seqlen_bias, int bt_width,
-                           int batch, int* off, int* max_steps) {
+                           int batch, int* off, int* max_steps,
+                           const int64_t* __restrict__ positions = nullptr, int64_t max_pos = 0,
+                           int* pos_out = nullptr) {
   __shared__ int wave_tot[THREADS / 64];
   __shared__ int wave_max[THREADS / 64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -96,6 +108,10 @@ __device__ void scan_steps(const int32_t* __restrict__ seqlens, int seqlen_bias,
     if (b < batch) {
       int L = seqlens[b] + seqlen_bias;
       L = max(0, min(L, bt_width * kPage));
+      if (positions) {
+        const int64_t p = positions[b];
+        pos_out[b] = (int)(p < 0 ? 0 : (p >= max_pos ? max_pos - 1 : p));
+      }
       off[b] = mine;
       const int steps = (L + TS - 1) / TS;
       mine += steps;
@@ -141,18 +157,77 @@ __device__ __forceinline__ bool use_unit_mode(int64_t total, int max_steps, int6
   return (int64_t)max_steps * 10 <= share * 11;
 }
 
+// Per-head QK-RMSNorm + RoPE of one lane's 8 consecutive dims d0 .. d0+7 of a
+// head (d0 = 8 * (lane16)), the 16 lanes of a DPP row holding the head: the
+// sum of squares is a row reduction and the RoPE partner of dim d (d < 64) is
+// dim d + 64, i.e. lane16 ^ 8 (a row rotation by 8).  c / s: cos / sin of the
+// token's position at the pair index d % 64.  Same expressions and rounding
+// points as qk_norm_rope_kernel (norm output rounded to bf16 before RoPE).
+__device__ __forceinline__ void norm_rope8(uint32_t x[4], const uint4 w, const float c[8],
+                                           const float s[8], float eps, bool upper) {
+  float xv[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    xv[2 * e] = bf16_lo(x[e]);
+    xv[2 * e + 1] = bf16_hi(x[e]);
+  }
+  const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss += xv[e] * xv[e];
+  ss = row16_sum(ss);
+  const float inv = rsqrtf(ss / (float)kHeadDim + eps);
+  float n[8], p[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    n[2 * e] = bf16_to_f32(f32_to_bf16(xv[2 * e] * inv * bf16_lo(ww[e])));
+    n[2 * e + 1] = bf16_to_f32(f32_to_bf16(xv[2 * e + 1] * inv * bf16_hi(ww[e])));
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) p[e] = dpp_f32<kDppRowRor8>(n[e]);
+  float o[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = upper ? n[e] * c[e] + p[e] * s[e] : n[e] * c[e] - p[e] * s[e];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) x[e] = pack_bf16x2(o[2 * e], o[2 * e + 1]);
+}
+
+// Inputs of the form with the QK-norm / RoPE / KV store folded in (the
+// kernel's q pointer is then the packed qkv rows, head stride 128).
+struct QkvArgs {
+  const uint16_t* q_w;       // q_norm weight [128]
+  const uint16_t* k_w;       // k_norm weight [128]
+  const int64_t* positions;  // [batch]
+  const float* cos_sin;      // [max_pos, 128]: cos(p f_i) at i, sin(p f_i) at 64 + i
+  int64_t max_pos;
+  const int32_t* slots;      // [batch]; outside [0, n_slots) skips the store
+  int64_t n_slots;
+  uint16_t* k_store;         // the caches, written at the new token's slot
+  uint16_t* v_store;
+  float eps;
+};
+
 // Grid: max(n_bal, units) workgroups.  n_bal = the balanced split's workgroup
 // count (two per CU), which also indexes the partial slots; the step offsets
 // and the mode word follow the slots of n_bal workgroups.
-template <int HKV, int G, int HG>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(G <= 2 ? 4 : 2)))
+//
+// QKV: q points at the packed [batch, (HQ + 2 HKV) * 128] qkv rows.  The q
+// heads are normalised and rotated when a segment starts; the workgroup whose
+// segment holds a unit's last step also normalises and rotates the new
+// token's k heads of the unit, writes them and the v heads to cache row
+// slots[b] (the lanes of token group 0), and, when slots[b] is the table slot
+// of key L - 1, uses them in place of that key's loaded row — the result of
+// storing first and attending afterwards, without a second launch.
+template <int HKV, int G, int HG, bool QKV>
+__global__ __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(G <= 2 ? (QKV ? QMI_QKV_WAVES_PER_EU : 4) : 2)))
 void decode_streamk_split(
     const uint16_t* __restrict__ q, int64_t q_seq_stride, int64_t q_head_stride,
     const uint16_t* __restrict__ k_cache, const uint16_t* __restrict__ v_cache,
     int64_t num_blocks, const int32_t* __restrict__ seqlens, int seqlen_bias,
     const int32_t* __restrict__ block_table, int64_t bt_stride, int bt_width, int batch,
     int n_bal, float scale_log2, uint16_t* __restrict__ out, int64_t out_seq_stride,
-    int64_t out_head_stride, float* __restrict__ ws, int force_units) {
+    int64_t out_head_stride, float* __restrict__ ws, int force_units, QkvArgs qa) {
   constexpr int NHG = HKV / HG;                          // units (head groups) per sequence
   constexpr int TG = kTokGroups<HG>;
   constexpr int TS = kStepTokens<HG>;
@@ -171,7 +246,12 @@ void decode_streamk_split(
   const int tg = tid / (16 * HG);
   const int64_t w = blockIdx.x;
 
-  scan_steps<kThreads, TS>(seqlens, seqlen_bias, bt_width, batch, off, &sm_max_steps);
+  __shared__ int sm_pos[QKV ? kMaxSeqScan : 1];
+  if constexpr (QKV)
+    scan_steps<kThreads, TS>(seqlens, seqlen_bias, bt_width, batch, off, &sm_max_steps,
+                             qa.positions, qa.max_pos, sm_pos);
+  else
+    scan_steps<kThreads, TS>(seqlens, seqlen_bias, bt_width, batch, off, &sm_max_steps);
   const int64_t total = (int64_t)NHG * off[batch];      // unit steps of the launch
   const int64_t n_units = (int64_t)batch * NHG;
   // Whole units are forced by the caller (no merge launch follows) or chosen
@@ -239,6 +319,11 @@ void decode_streamk_split(
                               (int64_t)(h * G + g) * q_head_stride + lane16 * 8);
       qw[g][0] = v.x; qw[g][1] = v.y; qw[g][2] = v.z; qw[g][3] = v.w;
     }
+    // QKV: the new token's rotated k and its v (this lane's 8 dims of head
+    // h), and whether key L - 1 is read from them.
+    [[maybe_unused]] uint4 k_new = make_uint4(0u, 0u, 0u, 0u), v_new = make_uint4(0u, 0u, 0u, 0u);
+    [[maybe_unused]] int32_t slot_new = -1;
+    [[maybe_unused]] const bool last_seg = seg_end == sb + steps_b;
     float m[G], l[G], acc[G][8];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -254,7 +339,11 @@ void decode_streamk_split(
     int32_t blk = bt_row[cur_page];
     int32_t blk_next = cur_page + 1 < bt_width ? bt_row[cur_page + 1] : -1;
 
-    for (int64_t st = s; st < seg_end; ++st) {
+    // One step of the segment.  In the form with the epilogue folded in, the
+    // segment's first step (FIRST: the epilogue) and the unit's last step
+    // (SUB: key L - 1 may be the new token) are peeled off the loop, so the
+    // steps in between run the plain loop body.
+    auto step = [&](int64_t st, auto first_c, auto sub_c) {
       const int tok0 = (int)(st - sb) * TS;               // first token of the step
       const int page = tok0 / kPage;
       if (page != cur_page) {                             // wave-uniform
@@ -276,6 +365,57 @@ void decode_streamk_split(
       for (int i = 0; i < kTok; ++i) kr[i] = load_u4_stream(kp + (o0 + (uint32_t)(i * kRowBytes)));
 #pragma unroll
       for (int i = 0; i < kTok; ++i) vr[i] = load_u4_stream(vp + (o0 + (uint32_t)(i * kRowBytes)));
+      if constexpr (QKV) {
+        if constexpr (decltype(first_c)::value) {
+          // The segment's first step: with its K/V loads on their way, load
+          // the RoPE row (position from LDS) and the norm weights, then
+          // normalise and rotate q (and the new token's k).
+          const float* cs = qa.cos_sin + (int64_t)sm_pos[b] * kHeadDim + 8 * (lane16 & 7);
+          const f32x4_t c0 = *reinterpret_cast<const f32x4_t*>(cs);
+          const f32x4_t c1 = *reinterpret_cast<const f32x4_t*>(cs + 4);
+          const f32x4_t s0 = *reinterpret_cast<const f32x4_t*>(cs + 64);
+          const f32x4_t s1 = *reinterpret_cast<const f32x4_t*>(cs + 68);
+          const uint4 wq = load_u4(qa.q_w + lane16 * 8);
+          uint4 kraw = make_uint4(0u, 0u, 0u, 0u), wk = make_uint4(0u, 0u, 0u, 0u);
+          if (last_seg) {  // wave-uniform
+            const uint16_t* src = q + (int64_t)b * q_seq_stride + lane16 * 8;
+            kraw = load_u4(src + (int64_t)(HQ + h) * kHeadDim);
+            v_new = load_u4(src + (int64_t)(HQ + HKV + h) * kHeadDim);
+            wk = load_u4(qa.k_w + lane16 * 8);
+            slot_new = qa.slots[b];
+          }
+          const float c[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+          const float sn[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+          const bool upper = lane16 >= 8;
+#pragma unroll
+          for (int g = 0; g < G; ++g) norm_rope8(qw[g], wq, c, sn, qa.eps, upper);
+          if (last_seg) {
+            uint32_t kw4[4] = {kraw.x, kraw.y, kraw.z, kraw.w};
+            norm_rope8(kw4, wk, c, sn, qa.eps, upper);
+            k_new = make_uint4(kw4[0], kw4[1], kw4[2], kw4[3]);
+            if (tg == 0 && slot_new >= 0 && slot_new < qa.n_slots) {
+              // One token group writes the unit's heads (non-temporal, as the KV store).
+              const int64_t row = ((int64_t)slot_new * HKV + h) * kHeadDim + lane16 * 8;
+              __builtin_nontemporal_store(*reinterpret_cast<const u32x4_t*>(&k_new),
+                                          reinterpret_cast<u32x4_t*>(qa.k_store + row));
+              __builtin_nontemporal_store(*reinterpret_cast<const u32x4_t*>(&v_new),
+                                          reinterpret_cast<u32x4_t*>(qa.v_store + row));
+            }
+          }
+        }
+        // Key L - 1 is the new token when this call stores it at the row the
+        // table maps it to: use the computed rows instead of the loaded ones.
+        if (decltype(sub_c)::value && last_seg && st == seg_end - 1 && page_ok &&
+            (int64_t)slot_new == (int64_t)blk * kPage + (L - 1) % kPage) {  // wave-uniform
+#pragma unroll
+          for (int i = 0; i < kTok; ++i) {
+            if (tok0 + tg * kTok + i == L - 1) {
+              kr[i] = k_new;
+              vr[i] = v_new;
+            }
+          }
+        }
+      }
       const bool partial = n_valid < TS;                 // wave-uniform
       if (partial) {
 #pragma unroll
@@ -338,6 +478,16 @@ void decode_streamk_split(
           for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(sc[g][i], v[e], acc[g][e]);
         }
       }
+    };
+    using yes = std::integral_constant<bool, true>;
+    using no = std::integral_constant<bool, false>;
+    if constexpr (QKV) {
+      step(s, yes{}, yes{});
+      const int64_t stop = last_seg ? seg_end - 1 : seg_end;
+      for (int64_t st = s + 1; st < stop; ++st) step(st, no{}, no{});
+      if (last_seg && seg_end - 1 > s) step(seg_end - 1, no{}, yes{});
+    } else {
+      for (int64_t st = s; st < seg_end; ++st) step(st, no{}, no{});
     }
 
     // ---- merge the token groups of this segment through LDS ----
@@ -601,17 +751,17 @@ bool streamk_supported(int64_t num_q_heads, int64_t num_kv_heads, int64_t batch)
   return hkv_ok && (g == 1 || g == 2 || g == 4) && batch <= 65535;
 }
 
-template <int HKV, int G, int HG>
+template <int HKV, int G, int HG, bool QKV>
 static int launch(const uint16_t* q, int64_t qs, int64_t qh, const uint16_t* kc, const uint16_t* vc,
                   int64_t nb, const int32_t* lens, int32_t bias, const int32_t* bt, int64_t bts,
                   int64_t btw, int64_t batch, float scale_log2, uint16_t* out, int64_t os,
-                  int64_t oh, float* ws, bool whole_units, hipStream_t s) {
+                  int64_t oh, float* ws, bool whole_units, const QkvArgs& qa, hipStream_t s) {
   const int64_t n_bal = streamk_balanced_wgs(batch, HKV, HG, btw);
   const int64_t n_units = batch * (HKV / HG);
   const int64_t grid = n_bal > n_units ? n_bal : n_units;
-  hipLaunchKernelGGL((decode_streamk_split<HKV, G, HG>), dim3((unsigned)grid), dim3(kThreads), 0, s,
-                     q, qs, qh, kc, vc, nb, lens, (int)bias, bt, bts, (int)btw, (int)batch,
-                     (int)n_bal, scale_log2, out, os, oh, ws, whole_units ? 1 : 0);
+  hipLaunchKernelGGL((decode_streamk_split<HKV, G, HG, QKV>), dim3((unsigned)grid), dim3(kThreads),
+                     0, s, q, qs, qh, kc, vc, nb, lens, (int)bias, bt, bts, (int)btw, (int)batch,
+                     (int)n_bal, scale_log2, out, os, oh, ws, whole_units ? 1 : 0, qa);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
   if (whole_units) return QMI_OK;  // every unit was written whole, empty ones as zeros
@@ -627,18 +777,19 @@ static int launch(const uint16_t* q, int64_t qs, int64_t qh, const uint16_t* kc,
   QMI_RETURN_LAUNCH_STATUS();
 }
 
-int launch_streamk(const uint16_t* q, int64_t qs, int64_t qh, const uint16_t* kc,
-                   const uint16_t* vc, int64_t nb, int64_t num_q_heads, int64_t num_kv_heads,
-                   const int32_t* lens, int32_t bias, const int32_t* bt, int64_t bts, int64_t btw,
-                   int64_t batch, float scale, uint16_t* out, int64_t os, int64_t oh, float* ws,
-                   bool whole_units, hipStream_t s) {
+template <bool QKV>
+static int launch_sk(const uint16_t* q, int64_t qs, int64_t qh, const uint16_t* kc,
+                     const uint16_t* vc, int64_t nb, int64_t num_q_heads, int64_t num_kv_heads,
+                     const int32_t* lens, int32_t bias, const int32_t* bt, int64_t bts,
+                     int64_t btw, int64_t batch, float scale, uint16_t* out, int64_t os,
+                     int64_t oh, float* ws, bool whole_units, const QkvArgs& qa, hipStream_t s) {
   const float sl = scale * kLog2e;
   const int64_t g = num_q_heads / num_kv_heads;
   const int64_t hg = streamk_heads_per_unit(batch, num_kv_heads);
 #define QMI_SK(HK, GG, HGG)                                                                      \
   if (num_kv_heads == HK && g == GG && hg == HGG)                                                \
-    return launch<HK, GG, HGG>(q, qs, qh, kc, vc, nb, lens, bias, bt, bts, btw, batch, sl, out, os, \
-                               oh, ws, whole_units, s);
+    return launch<HK, GG, HGG, QKV>(q, qs, qh, kc, vc, nb, lens, bias, bt, bts, btw, batch, sl,   \
+                                    out, os, oh, ws, whole_units, qa, s);
 #define QMI_SK_G(HK, HGG) QMI_SK(HK, 1, HGG) QMI_SK(HK, 2, HGG) QMI_SK(HK, 4, HGG)
   QMI_SK_G(8, 8) QMI_SK_G(8, 4) QMI_SK_G(8, 2)
   QMI_SK_G(4, 4) QMI_SK_G(4, 2)
@@ -649,4 +800,52 @@ int launch_streamk(const uint16_t* q, int64_t qs, int64_t qh, const uint16_t* kc
   return QMI_E_UNSUPPORTED;
 }
 
+int launch_streamk(const uint16_t* q, int64_t qs, int64_t qh, const uint16_t* kc,
+                   const uint16_t* vc, int64_t nb, int64_t num_q_heads, int64_t num_kv_heads,
+                   const int32_t* lens, int32_t bias, const int32_t* bt, int64_t bts, int64_t btw,
+                   int64_t batch, float scale, uint16_t* out, int64_t os, int64_t oh, float* ws,
+                   bool whole_units, hipStream_t s) {
+  return launch_sk<false>(q, qs, qh, kc, vc, nb, num_q_heads, num_kv_heads, lens, bias, bt, bts,
+                          btw, batch, scale, out, os, oh, ws, whole_units, QkvArgs{}, s);
+}
+
 }  // namespace qmi
+
+static inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+extern "C" int qmi_paged_decode_attention_qkv(
+    const uint16_t* qkv, int64_t qkv_stride, int64_t num_q_heads, int64_t num_kv_heads,
+    int64_t head_dim, const uint16_t* q_norm_weight, const uint16_t* k_norm_weight,
+    const int64_t* positions, const float* cos_sin_cache, int64_t max_position, float eps,
+    uint16_t* k_cache, uint16_t* v_cache, int64_t num_blocks, int64_t block_size,
+    const int32_t* slot_mapping, const int32_t* seqlens, const int32_t* block_table,
+    int64_t bt_stride, int64_t bt_width, int64_t batch, float scale, uint16_t* out,
+    int64_t out_seq_stride, int64_t out_head_stride, float* workspace, int64_t workspace_bytes,
+    int64_t pages_per_split, void* stream) {
+  if (batch < 0 || num_blocks < 0 || bt_width < 0 || max_position <= 0) return QMI_E_BAD_SHAPE;
+  if (batch == 0) return QMI_OK;
+  if (num_blocks == 0 || bt_width == 0) return QMI_E_BAD_SHAPE;
+  if (!qkv || !q_norm_weight || !k_norm_weight || !positions || !cos_sin_cache || !k_cache ||
+      !v_cache || !slot_mapping || !seqlens || !block_table || !out)
+    return QMI_E_NULL_POINTER;
+  if (head_dim != kHeadDim || block_size != kPage) return QMI_E_UNSUPPORTED;
+  if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads != 0)
+    return QMI_E_BAD_SHAPE;
+  if (pages_per_split > 0 || pages_per_split < -1) return QMI_E_UNSUPPORTED;
+  if (!qmi::streamk_supported(num_q_heads, num_kv_heads, batch) || bt_width > 65535)
+    return QMI_E_UNSUPPORTED;
+  if (bt_stride < bt_width) return QMI_E_BAD_STRIDE;
+  if (qkv_stride < (num_q_heads + 2 * num_kv_heads) * kHeadDim || qkv_stride % 8 || !al16(qkv) ||
+      !al16(q_norm_weight) || !al16(k_norm_weight) || !al16(cos_sin_cache) || !al16(k_cache) ||
+      !al16(v_cache) || !al16(out) || out_seq_stride % 8 || out_head_stride % 8)
+    return QMI_E_BAD_STRIDE;
+  const int64_t need = qmi::streamk_workspace_bytes(batch, num_q_heads, num_kv_heads, bt_width);
+  if (!workspace || workspace_bytes < need) return QMI_E_WORKSPACE_TOO_SMALL;
+  const QkvArgs qa{q_norm_weight, k_norm_weight, positions, cos_sin_cache, max_position,
+                   slot_mapping, num_blocks * kPage, k_cache, v_cache, eps};
+  return qmi::launch_sk<true>(qkv, qkv_stride, kHeadDim, k_cache, v_cache, num_blocks,
+                              num_q_heads, num_kv_heads, seqlens, 1, block_table, bt_stride,
+                              bt_width, batch, scale, out, out_seq_stride, out_head_stride,
+                              workspace, pages_per_split == -1, qa,
+                              reinterpret_cast<hipStream_t>(stream));
+}

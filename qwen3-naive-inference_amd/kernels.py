@@ -148,6 +148,89 @@ def paged_decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
     return out
 
 
+def decode_qkv_ok(num_q_heads: int, num_kv_heads: int, head_dim: int, batch: int) -> bool:
+    """Whether ``paged_decode_attention_qkv`` takes this layout and batch."""
+    return (head_dim == HEAD_DIM and num_kv_heads in (2, 4, 8, 16)
+            and num_q_heads % num_kv_heads == 0 and num_q_heads // num_kv_heads in (1, 2, 4)
+            and 0 < batch <= 1024)
+
+
+def paged_decode_attention_qkv(qkv: torch.Tensor, q_norm_weight: torch.Tensor,
+                               k_norm_weight: torch.Tensor, positions: torch.Tensor,
+                               cos_sin_cache: torch.Tensor, num_q_heads: int, num_kv_heads: int,
+                               eps: float, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                               slot_mapping: torch.Tensor, cache_seqlens: torch.Tensor,
+                               block_table: torch.Tensor, softmax_scale: float,
+                               out: torch.Tensor | None = None,
+                               pages_per_split: int = 0) -> torch.Tensor:
+    """``qk_norm_rope_store`` followed by ``paged_decode_attention(...,
+    seqlen_bias=1)`` in one attention launch: the q heads of the packed
+    ``qkv [B, (Hq + 2 Hkv) * 128]`` rows are normalised and rotated inside
+    the attention kernel, and the new token's rotated k and its v go to cache
+    rows ``slot_mapping`` (-1 skips; otherwise the slot of key
+    ``cache_seqlens[b]``, which is then read from the new rows).  Returns
+    ``out [B, Hq, 128]``.  ``pages_per_split``: 0 (balanced split + merge)
+    or -1 (one whole unit per workgroup, no merge launch)."""
+    _require_cuda("qkv", qkv)
+    _require_dtype("qkv", qkv, torch.bfloat16)
+    width = (num_q_heads + 2 * num_kv_heads) * HEAD_DIM
+    if qkv.dim() != 2 or qkv.shape[1] != width:
+        raise ValueError(f"qkv must be [B, {width}]")
+    if qkv.stride(1) != 1 or qkv.stride(0) % 8 or qkv.data_ptr() % 16:
+        qkv = _dense16(qkv)
+    bsz = qkv.shape[0]
+    for n, t in (("k_cache", k_cache), ("v_cache", v_cache)):
+        _require_cuda(n, t)
+        _require_dtype(n, t, torch.bfloat16)
+    if (k_cache.dim() != 4 or k_cache.shape != v_cache.shape or not k_cache.is_contiguous()
+            or not v_cache.is_contiguous()):
+        raise ValueError("caches must be contiguous [num_blocks, 256, Hkv, 128] of equal shape")
+    nb, bs, hkv, dk = k_cache.shape
+    if bs != BLOCK_SIZE or dk != HEAD_DIM or hkv != num_kv_heads:
+        raise ValueError(f"caches must be [num_blocks, {BLOCK_SIZE}, {num_kv_heads}, {HEAD_DIM}]")
+    if pages_per_split not in (0, -1):
+        raise ValueError("pages_per_split must be 0 or -1 (balanced schedule)")
+    for n, t in (("positions", positions), ("cos_sin_cache", cos_sin_cache),
+                 ("q_norm_weight", q_norm_weight), ("k_norm_weight", k_norm_weight)):
+        _require_cuda(n, t)
+    cache = cos_sin_cache
+    if cache.dtype != torch.float32 or cache.dim() != 2 or cache.shape[1] != HEAD_DIM:
+        raise ValueError("cos_sin_cache must be fp32 [max_position, 128]")
+    cache = _dense16(cache)
+    pos = positions.reshape(-1)
+    if pos.dtype != torch.int64:
+        pos = pos.to(torch.int64)
+    sl = _as_i32("slot_mapping", slot_mapping).reshape(-1)
+    seqlens = _as_i32("cache_seqlens", cache_seqlens).reshape(-1)
+    if pos.shape[0] != bsz or sl.shape[0] != bsz or seqlens.shape[0] != bsz:
+        raise ValueError(f"positions, slot_mapping and cache_seqlens must have {bsz} entries")
+    pos, sl, seqlens = pos.contiguous(), sl.contiguous(), seqlens.contiguous()
+    bt = _as_i32("block_table", block_table)
+    if bt.dim() != 2 or bt.shape[0] != bsz or bt.shape[1] < 1:
+        raise ValueError(f"block_table must be [{bsz}, W>=1], got {tuple(bt.shape)}")
+    if bt.stride(1) != 1:
+        bt = bt.contiguous()
+    qw = _dense16(q_norm_weight.to(torch.bfloat16))
+    kw = _dense16(k_norm_weight.to(torch.bfloat16))
+    if out is None:
+        out = torch.empty((bsz, num_q_heads, HEAD_DIM), dtype=torch.bfloat16, device=qkv.device)
+    elif out.shape != (bsz, num_q_heads, HEAD_DIM) or out.stride(2) != 1:
+        raise ValueError("out must be [B, Hq, 128] with unit stride along the head dim")
+    if bsz == 0:
+        return out
+    L = lib()
+    wbytes = L.qmi_paged_decode_workspace_bytes(bsz, num_kv_heads, num_q_heads, bt.shape[1], 0)
+    ws = torch.empty((max(wbytes, 4) // 4,), dtype=torch.float32, device=qkv.device)
+    check(L.qmi_paged_decode_attention_qkv(
+        qkv.data_ptr(), qkv.stride(0), num_q_heads, num_kv_heads, HEAD_DIM, qw.data_ptr(),
+        kw.data_ptr(), pos.data_ptr(), cache.data_ptr(), cache.shape[0], float(eps),
+        k_cache.data_ptr(), v_cache.data_ptr(), nb, bs, sl.data_ptr(), seqlens.data_ptr(),
+        bt.data_ptr(), bt.stride(0), bt.shape[1], bsz, float(softmax_scale), out.data_ptr(),
+        out.stride(0), out.stride(1), ws.data_ptr(), ws.numel() * 4, int(pages_per_split),
+        stream_handle(qkv.device)), "paged_decode_attention_qkv")
+    return out
+
+
 # ---------------------------------------------------------------------------
 # Varlen paged causal prefill (flash_attn_varlen_func at qwen3_naive.py:631-637)
 # ---------------------------------------------------------------------------
@@ -327,6 +410,9 @@ def qk_norm_rope(qkv: torch.Tensor, q_norm_weight: torch.Tensor, k_norm_weight: 
     if qkv.data_ptr() % 16 or qkv.stride(0) % 8:
         qkv = _dense16(qkv)  # the kernel reads rows 8 / 16 bytes at a time
     n = qkv.shape[0]
+    for nm, t in (("positions", positions), ("cos_sin_cache", cos_sin_cache),
+                  ("q_norm_weight", q_norm_weight), ("k_norm_weight", k_norm_weight)):
+        _require_cuda(nm, t)
     pos = positions.reshape(-1)
     if pos.dtype != torch.int64:
         pos = pos.to(torch.int64)
@@ -364,6 +450,9 @@ def qk_norm_rope_store(qkv: torch.Tensor, q_norm_weight: torch.Tensor,
     if qkv.data_ptr() % 16 or qkv.stride(0) % 8:
         qkv = _dense16(qkv)  # the kernel reads rows 8 / 16 bytes at a time
     n = qkv.shape[0]
+    for nm, t in (("positions", positions), ("cos_sin_cache", cos_sin_cache),
+                  ("q_norm_weight", q_norm_weight), ("k_norm_weight", k_norm_weight)):
+        _require_cuda(nm, t)
     pos = positions.reshape(-1)
     if pos.dtype != torch.int64:
         pos = pos.to(torch.int64)

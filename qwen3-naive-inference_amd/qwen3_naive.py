@@ -176,6 +176,10 @@ class Qwen3Attention(nn.Module):
         # with merge, -1 = one whole (sequence, head group) unit per
         # workgroup and no merge (the engine picks it for near-equal contexts).
         self.decode_pages_per_split = 0
+        # Decode steps fold the QK-norm / RoPE / KV store into the attention
+        # launch (qmi_paged_decode_attention_qkv); False runs them as the
+        # separate fused norm kernel before the attention.
+        self.decode_fused_qkv = True
         # Not a registered submodule: the cache is shared between layers.
         self.__dict__["rotary_emb"] = get_rope(self.head_dim, config.max_position_embeddings,
                                                config.rope_theta)
@@ -248,10 +252,19 @@ class Qwen3Attention(nn.Module):
             ctx = context_lens.long()
             blk = block_tables.long().gather(1, (ctx // BLOCK_SIZE)[:, None])[:, 0]
             slot_mapping = (blk * BLOCK_SIZE + ctx % BLOCK_SIZE).to(torch.int32)
-        q = self._project_store(x, positions, slot_mapping, decode=True)
-        o = K.paged_decode_attention(q, self.k_cache, self.v_cache, context_lens, block_tables,
-                                     self.scale, seqlen_bias=1,
-                                     pages_per_split=self.decode_pages_per_split)
+        if (self.decode_fused_qkv and self.decode_pages_per_split <= 0 and _use_kernels(x)
+                and K.decode_qkv_ok(self.num_heads, self.num_kv_heads, self.head_dim, batch)):
+            qkv = _decode_linear(self.qkv_proj, x)
+            o = K.paged_decode_attention_qkv(
+                qkv, self.q_norm.weight, self.k_norm.weight, positions, self._cos_sin(x.device),
+                self.num_heads, self.num_kv_heads, self.eps, self.k_cache, self.v_cache,
+                slot_mapping, context_lens, block_tables, self.scale,
+                pages_per_split=self.decode_pages_per_split)
+        else:
+            q = self._project_store(x, positions, slot_mapping, decode=True)
+            o = K.paged_decode_attention(q, self.k_cache, self.v_cache, context_lens,
+                                         block_tables, self.scale, seqlen_bias=1,
+                                         pages_per_split=self.decode_pages_per_split)
         return _decode_linear(self.o_proj, o.view(batch, -1), parts=True)
 
 
