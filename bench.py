@@ -923,7 +923,7 @@ def _timed(torch, fn):
 
 
 def leg_rollout(torch, pkg, dev, new_tokens=1024, compare_tokens=64, preempt_blocks=1200,
-                engines=("ours", "kernels", "torch")):
+                engines=("ours", "kernels", "torch"), runs_n=3, cpu=False):
     """Config 5: 32 prompts x group 8 = 256 sequences, 128-token prompts, T=1.0,
     no top-k, ``new_tokens`` generated tokens each, continuous batching with the
     2048-token step budget and LIFO preemption, ~40 GB pool (1,362 blocks: no
@@ -963,20 +963,29 @@ def leg_rollout(torch, pkg, dev, new_tokens=1024, compare_tokens=64, preempt_blo
         del model
         torch.cuda.empty_cache()
         return out
-    log(f"rollout: full run ({n_tok} x {new_tokens} tokens)")
-    torch.manual_seed(2)
-    (toks, gen_t, lps, plens), t_roll = _timed(torch, lambda: gen(new_tokens))
-    stats = dict(model.last_stats)
-    t0 = time.perf_counter()
-    loss = grpo_loss_after_rollout(torch, pkg, model, toks, plens, lps, 32, 8)
-    torch.cuda.synchronize()
-    t_loss = time.perf_counter() - t0
-    generated = sum(len(x) for x in gen_t)
-    assert len(set(len(x) for x in toks)) == 1, "fixed-length rollout expected (no EOS)"
-    out.update(dict(generated=generated, rollout_s=t_roll, loss_s=t_loss, loss=loss,
-                    tokens_per_s=generated / t_roll, tokens_per_s_with_loss=generated / (t_roll + t_loss),
-                    num_blocks=model._num_blocks, **stats))
-    del toks, gen_t, lps
+    # Three timed runs (rollout, then the loss over its tokens), median reported;
+    # the short capture run above is the warm-up.
+    runs = []
+    for i in range(runs_n):
+        log(f"rollout: full run {i + 1}/{runs_n} ({n_tok} x {new_tokens} tokens)")
+        torch.manual_seed(2 + i)
+        (toks, gen_t, lps, plens), t_roll = _timed(torch, lambda: gen(new_tokens))
+        stats = dict(model.last_stats)
+        t0 = time.perf_counter()
+        loss = grpo_loss_after_rollout(torch, pkg, model, toks, plens, lps, 32, 8)
+        torch.cuda.synchronize()
+        t_loss = time.perf_counter() - t0
+        generated = sum(len(x) for x in gen_t)
+        assert len(set(len(x) for x in toks)) == 1, "fixed-length rollout expected (no EOS)"
+        runs.append(dict(rollout_s=t_roll, loss_s=t_loss, loss=loss, stats=stats))
+        del toks, gen_t, lps
+    med = sorted(runs, key=lambda r: r["rollout_s"])[len(runs) // 2]
+    t_roll, t_loss = med["rollout_s"], med["loss_s"]
+    out.update(dict(generated=generated, rollout_s=t_roll, loss_s=t_loss, loss=med["loss"],
+                    tokens_per_s=generated / t_roll,
+                    tokens_per_s_with_loss=generated / (t_roll + t_loss),
+                    runs_tokens_per_s=[generated / r["rollout_s"] for r in runs],
+                    num_blocks=model._num_blocks, **med["stats"]))
     if preempt_blocks:
         log(f"rollout: {preempt_blocks}-block pool (forced LIFO preemption)")
         model.allocate_global_kv_cache(num_blocks=preempt_blocks)
@@ -990,9 +999,46 @@ def leg_rollout(torch, pkg, dev, new_tokens=1024, compare_tokens=64, preempt_blo
                               **dict(model.last_stats))
         log(f"rollout: preemption run {gen_n / dt:.0f} tok/s, "
             f"{model.last_stats['preemptions']} preemptions")
+    if cpu:
+        log("cpu baseline (oracle decode steps at batch 256)")
+        out["cpu_baseline"] = cpu_baseline_rollout(torch, model)
     del model
     torch.cuda.empty_cache()
     return out
+
+
+def cpu_baseline_rollout(torch, model, steps=2, ctx=640, batch=256):
+    """Config 5 on the host cores, sampled: ``steps`` decode steps of the
+    oracle's 28-layer model (fp32 torch CPU, qwen3_decode_step) for ``batch``
+    sequences at the rollout's mean context (every sequence with ``ctx``
+    cached keys of random K/V, the same rows in every layer), the model's own
+    random-init weights; tokens/s = batch x steps / time."""
+    from oracle import model as OM
+    torch.set_num_threads(os.cpu_count() or 1)
+    cfg = model.config
+    sd = {k: v.detach().float().cpu() for k, v in model.state_dict().items()}  # fp32 once
+    g = torch.Generator().manual_seed(5)
+    k_rows = [torch.randn(ctx, cfg.num_key_value_heads, cfg.head_dim, generator=g)
+              .to(torch.bfloat16) for _ in range(batch)]
+    v_rows = [torch.randn(ctx, cfg.num_key_value_heads, cfg.head_dim, generator=g)
+              .to(torch.bfloat16) for _ in range(batch)]
+    k_ctx = [k_rows] * cfg.num_hidden_layers
+    v_ctx = [v_rows] * cfg.num_hidden_layers
+    tok = torch.randint(0, cfg.vocab_size, (batch,), generator=g)
+    pos = torch.full((batch,), ctx, dtype=torch.int64)
+    times = []
+    for _ in range(steps):
+        t = time.perf_counter()
+        OM.qwen3_decode_step(sd, tok, pos, k_ctx, v_ctx, cfg.num_hidden_layers,
+                             cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim,
+                             cfg.rms_norm_eps, cfg.rope_theta)
+        times.append(time.perf_counter() - t)
+    dt = statistics.median(times)
+    return dict(value=batch / dt, unit="tokens/s", cores=torch.get_num_threads(), kind="port",
+                sample=f"oracle 28-layer decode step (fp32 torch CPU) for {batch} sequences with "
+                       f"{ctx} cached keys each (the rollout's mean context), median of {steps} "
+                       f"steps",
+                seconds_per_sample=dt, cpu_model=_cpu_model())
 
 
 def leg_copy_calibration(torch, dev, nbytes=1 << 30):
@@ -1142,6 +1188,8 @@ def main() -> int:
                          "build's kernels), torch (reference loop, torch body)")
     ap.add_argument("--rollout-preempt-blocks", type=int, default=1200,
                     help="pool of the forced-preemption rollout (0 skips it)")
+    ap.add_argument("--rollout-runs", type=int, default=3,
+                    help="timed full rollouts (median reported)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 1 GiB device copy (counter calibration)")
@@ -1200,7 +1248,8 @@ def main() -> int:
         results["rollout"] = leg_rollout(torch, pkg, dev, new_tokens=args.rollout_tokens,
                                          compare_tokens=args.rollout_compare_tokens,
                                          preempt_blocks=args.rollout_preempt_blocks,
-                                         engines=tuple(args.rollout_engines.split(",")))
+                                         engines=tuple(args.rollout_engines.split(",")),
+                                         runs_n=args.rollout_runs, cpu=not args.no_cpu)
 
     cpu_grpo = None
     if not args.no_cpu and "grpo" in results:
@@ -1313,7 +1362,10 @@ def main() -> int:
             "loss_s": round(r["loss_s"], 3), "loss": r["loss"], "kv_blocks": r["num_blocks"],
             "preemptions": r.get("preemptions"), "engine_steps": r.get("steps"),
             "graph_decode_steps": r.get("graph_steps"),
-            "lookahead_decode_steps": r.get("lookahead_steps")}
+            "lookahead_decode_steps": r.get("lookahead_steps"),
+            "runs": len(r["runs_tokens_per_s"]),
+            "runs_tokens_per_s": [round(x, 1) for x in r["runs_tokens_per_s"]],
+            "cpu_baseline": r.get("cpu_baseline")}
         if "preempt" in r:
             pr = r["preempt"]
             secondary["grpo_rollout"]["forced_preemption"] = {
