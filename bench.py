@@ -179,7 +179,7 @@ def make_qwen3(torch, pkg, dev, seed=0):
 def leg_decode_step(torch, pkg, dev, steps, warmup, w, attn_ms_step):
     """Config 3 as a whole: one 28-layer Qwen3-0.6B decode step for the
     64-sequence serving batch (embedding, per layer add+RMSNorm, qkv GEMM,
-    fused QK-norm/RoPE/KV store, paged attention, o GEMM, add+RMSNorm,
+    paged attention with the QK-norm/RoPE/KV store folded in, o GEMM, add+RMSNorm,
     gate_up GEMM, SwiGLU, down GEMM; final norm), captured as the engine's
     HIP graph and replayed; then the lm_head and the fused sampler.  Uses the
     decode leg's 28-layer pools, contexts and page tables (``w``)."""
@@ -1305,8 +1305,8 @@ def main() -> int:
         secondary["decode_step_28layer_b64"] = {
             "workload": "one full Qwen3-0.6B decode step (28 layers, random-init bf16 weights) "
                         "for 64 sequences, contexts U{1024..4096}, shuffled page tables, as the "
-                        "engine's HIP graph (embedding, norms, GEMMs, fused QK-norm/RoPE/KV "
-                        "store, paged attention, SwiGLU, final norm); the fused lm_head + sampler "
+                        "engine's HIP graph (embedding, norms, GEMMs, paged attention with the "
+                        "QK-norm/RoPE/KV store folded in, SwiGLU, final norm); the fused lm_head + sampler "
                         "(logits never materialised) timed after it; the unfused [64, V] lm_head "
                         "GEMM alone for comparison",
             "ms_per_step": round(r["ms_per_step"], 4),
