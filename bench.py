@@ -874,12 +874,13 @@ def rollout_prompts(torch, n_prompts=32, group=8, prompt_len=128, vocab=151936, 
     return [p for p in base for _ in range(group)]
 
 
-def grpo_loss_after_rollout(torch, pkg, model, seqs, plens, lps, n_prompts, group, micro=16, seed=0):
+def grpo_loss_after_rollout(torch, pkg, model, seqs, plens, lps, n_prompts, group, micro=32, seed=0):
     """New log-probs of every generated token (prefill forward to the final
     hidden states, then the fused lm_head + log-prob kernel: no logits are
     materialised), seeded Bernoulli(0.5) rewards, group advantages and the
     clipped loss (per-sequence masked mean), next-token alignment;
-    micro-batched over sequences."""
+    micro-batched over sequences (32 sequences = 36,864 rows per forward: the
+    loss step took 0.567 / 0.537 / 0.540 s at 16 / 32 / 64)."""
     dev = next(model.parameters()).device
     g = torch.Generator().manual_seed(seed)
     rewards = torch.bernoulli(torch.full((len(seqs),), 0.5), generator=g).to(dev)
