@@ -54,6 +54,14 @@ constexpr int kKC = 64;             // hidden elements per staged chunk
 constexpr int kRowB = kKC * 2;      // bytes per staged row
 constexpr int kRowThreads = 256;    // kernel 2
 
+// Register sets of the load stream (steps of loads in flight).
+#ifndef QMI_LM_NSET_SMALL
+#define QMI_LM_NSET_SMALL 2
+#endif
+#ifndef QMI_LM_NSET_LARGE
+#define QMI_LM_NSET_LARGE 2
+#endif
+
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
   return __builtin_bit_cast(bf16x8_t, u32x4_t{v.x, v.y, v.z, v.w});
 }
@@ -61,7 +69,7 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
 // Byte offset of 16-byte piece c of staged row r.
 __device__ __forceinline__ int lds_off(int r, int c) { return r * kRowB + ((c ^ ((r >> 1) & 7)) << 4); }
 
-template <int MT, int NW, int NSTAGE>
+template <int MT, int NW, int NSTAGE, int NSET>
 __global__ __launch_bounds__(NW * 64) void lmhead_tiles(
     const uint16_t* __restrict__ h, int64_t h_stride, int n_rows,
     const uint16_t* __restrict__ w, int64_t w_stride, int vocab, int hidden, float c2,
@@ -113,39 +121,63 @@ __global__ __launch_bounds__(NW * 64) void lmhead_tiles(
     const int q = tid + i * NT;
     hdst[i] = W_BYTES + lds_off(q >> 3, q & 7);
   }
-  uint4 wreg[2][WCH], hreg[2][HCH];
-  int ld_tile = t_begin, ld_kc = 0, ld_step = 0;     // next step the load stream fetches
-  auto load_next = [&](auto set_c) __attribute__((always_inline)) {
-    constexpr int P = decltype(set_c)::value;
-    const int v0 = (ld_tile / n_rtiles) * kTV;
-    const int r0 = (ld_tile % n_rtiles) * MT;
+  uint4 wreg[NSET][WCH], hreg[NSET][HCH];
+  // Tile positions (vocabulary tile, row tile) advance incrementally: no
+  // division per step (a runtime division is a long scalar sequence, and at
+  // one instruction stream per wave it delays the MFMAs behind it).
+  struct Pos {
+    int vt, rt;
+  };
+  auto advance = [&](Pos p) -> Pos { return p.rt + 1 == n_rtiles ? Pos{p.vt + 1, 0} : Pos{p.vt, p.rt + 1}; };
+  const Pos p_begin{t_begin / n_rtiles, t_begin % n_rtiles};
+  // Load stream: the next step it fetches, and the current tile's bases and
+  // per-lane element offsets (rows past the vocabulary or the batch clamped to
+  // the tile's last valid row), set up once per tile.
+  Pos ld = p_begin;
+  int ld_kc = 0, ld_step = 0;
+  const uint16_t* wt0;
+  const uint16_t* ht0;
+  int woff[WCH], hoff[HCH];
+  auto ld_tile_setup = [&]() __attribute__((always_inline)) {
+    const int v0 = ld.vt * kTV, r0 = ld.rt * MT;
     const int wlast = min(kTV, vocab - v0) - 1;      // last valid row of the tile
     const int hlast = min(MT, n_rows - r0) - 1;
-    const uint16_t* wt = w + (int64_t)v0 * w_stride + ld_kc * kKC;
-    const uint16_t* ht = h + (int64_t)r0 * h_stride + ld_kc * kKC;
+    wt0 = w + (int64_t)v0 * w_stride;
+    ht0 = h + (int64_t)r0 * h_stride;
 #pragma unroll
     for (int i = 0; i < WCH; ++i) {
       const int q = tid + i * NT;
-      wreg[P][i] = load_u4_stream(wt + min(q >> 3, wlast) * (int)w_stride + (q & 7) * 8);
+      woff[i] = min(q >> 3, wlast) * (int)w_stride + (q & 7) * 8;
     }
 #pragma unroll
     for (int i = 0; i < HCH; ++i) {
       const int q = tid + i * NT;
-      hreg[P][i] = load_u4(ht + min(q >> 3, hlast) * (int)h_stride + (q & 7) * 8);
+      hoff[i] = min(q >> 3, hlast) * (int)h_stride + (q & 7) * 8;
     }
+  };
+  ld_tile_setup();
+  auto load_next = [&](auto set_c) __attribute__((always_inline)) {
+    constexpr int P = decltype(set_c)::value;
+    const uint16_t* wt = wt0 + ld_kc * kKC;
+    const uint16_t* ht = ht0 + ld_kc * kKC;
+#pragma unroll
+    for (int i = 0; i < WCH; ++i) wreg[P][i] = load_u4_stream(wt + woff[i]);
+#pragma unroll
+    for (int i = 0; i < HCH; ++i) hreg[P][i] = load_u4(ht + hoff[i]);
     if (ld_step + 1 < n_steps) {
       ++ld_step;
       if (++ld_kc == n_kc) {
         ld_kc = 0;
-        ++ld_tile;
+        ld = advance(ld);
+        ld_tile_setup();
       }
     }
   };
-  auto store_step = [&](int stage, int tile, auto set_c) __attribute__((always_inline)) {
+  auto store_step = [&](int stage, Pos tile, auto set_c) __attribute__((always_inline)) {
     constexpr int P = decltype(set_c)::value;
     unsigned char* base = lds + stage * STAGE;
-    const int wn = min(kTV, vocab - (tile / n_rtiles) * kTV);
-    const int hn = min(MT, n_rows - (tile % n_rtiles) * MT);
+    const int wn = min(kTV, vocab - tile.vt * kTV);
+    const int hn = min(MT, n_rows - tile.rt * MT);
 #pragma unroll
     for (int i = 0; i < WCH; ++i) {
       const int q = tid + i * NT;
@@ -185,8 +217,8 @@ __global__ __launch_bounds__(NW * 64) void lmhead_tiles(
   // Target mode: the target ids of this lane's four rows, loaded when a tile
   // starts (straight-line loads, consumed by the tile's epilogue).
   int64_t tgt_id[4] = {-1, -1, -1, -1};
-  auto load_targets = [&](int tile) __attribute__((always_inline)) {
-    const int r0 = (tile % n_rtiles) * MT;
+  auto load_targets = [&](Pos tile) __attribute__((always_inline)) {
+    const int r0 = tile.rt * MT;
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
       const int row = r0 + 64 * rq + 16 * rb + l16;
@@ -194,10 +226,10 @@ __global__ __launch_bounds__(NW * 64) void lmhead_tiles(
     }
   };
 
-  auto epilogue = [&](int tile) __attribute__((always_inline)) {
-    const int vt = tile / n_rtiles;
+  auto epilogue = [&](Pos tile) __attribute__((always_inline)) {
+    const int vt = tile.vt;
     const int64_t v0 = (int64_t)vt * kTV;
-    const int64_t r0 = (int64_t)(tile % n_rtiles) * MT;
+    const int64_t r0 = (int64_t)tile.rt * MT;
     const int64_t vbase = v0 + VW * vq + 4 * g4;
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
@@ -252,14 +284,17 @@ __global__ __launch_bounds__(NW * 64) void lmhead_tiles(
     }
   };
 
-  // Step st (chunk kc of tile `tile`): the loads of step st + 2 go into
-  // register set st % 2 (already in LDS), the MFMAs read stage st % 3, then
-  // set (st + 1) % 2 -- step st + 1, loaded one step earlier -- is written to
-  // stage (st + 1) % 3, which no wave has read since the barrier that ended
-  // step st - 1.
-  int tile = t_begin, kc = 0, stage = 0;
+  // Step st (chunk kc of tile `tile`): the loads of step st + NSET go into
+  // register set st % NSET (already in LDS), the MFMAs read stage
+  // st % NSTAGE, then set (st + 1) % NSET -- step st + 1, loaded NSET - 1
+  // steps earlier -- is written to stage (st + 1) % NSTAGE, which no wave has
+  // read since the barrier that ended step st - 1.  NSET - 1 steps of compute
+  // cover each load's latency.
+  Pos tile = p_begin;
+  int kc = 0, stage = 0;
   auto step = [&](int st, auto set_c) __attribute__((always_inline)) {
     constexpr int P = decltype(set_c)::value;
+    constexpr int PN = P + 1 == NSET ? 0 : P + 1;
     if (tgt && kc == 0) load_targets(tile);
     load_next(std::integral_constant<int, P>{});
     const unsigned char* base = lds + stage * STAGE;
@@ -279,8 +314,8 @@ __global__ __launch_bounds__(NW * 64) void lmhead_tiles(
           acc[vb][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[vb], b[rb], acc[vb][rb], 0, 0, 0);
     }
     const int next_stage = stage == NSTAGE - 1 ? 0 : stage + 1;
-    const int next_tile = kc + 1 == n_kc ? tile + 1 : tile;
-    if (st + 1 < n_steps) store_step(next_stage, next_tile, std::integral_constant<int, 1 - P>{});
+    const Pos next_tile = kc + 1 == n_kc ? advance(tile) : tile;
+    if (st + 1 < n_steps) store_step(next_stage, next_tile, std::integral_constant<int, PN>{});
     __syncthreads();
     if (kc + 1 == n_kc) epilogue(tile);
     stage = next_stage;
@@ -288,16 +323,14 @@ __global__ __launch_bounds__(NW * 64) void lmhead_tiles(
     kc = kc + 1 == n_kc ? 0 : kc + 1;
   };
 
-  load_next(std::integral_constant<int, 0>{});
-  load_next(std::integral_constant<int, 1>{});
-  store_step(0, t_begin, std::integral_constant<int, 0>{});
+  static_for<0, NSET>([&](auto i_c) __attribute__((always_inline)) { load_next(i_c); });
+  store_step(0, p_begin, std::integral_constant<int, 0>{});
   __syncthreads();
-  int st = 0;
-  for (; st + 1 < n_steps; st += 2) {
-    step(st, std::integral_constant<int, 0>{});
-    step(st + 1, std::integral_constant<int, 1>{});
+  for (int st = 0; st < n_steps; st += NSET) {
+    static_for<0, NSET>([&](auto i_c) __attribute__((always_inline)) {
+      if (st + (int)decltype(i_c)::value < n_steps) step(st + decltype(i_c)::value, i_c);
+    });
   }
-  if (st < n_steps) step(st, std::integral_constant<int, 0>{});
 }
 
 // Block-wide helpers for kernel 2 (256 threads).
@@ -526,19 +559,20 @@ int launch_tiles(const uint16_t* h, int64_t h_stride, int64_t n_rows, const uint
   // than three stages, and than 4 waves of 128 x 64 or two 128-row
   // workgroups per CU).  A persistent grid of that many workgroups per CU, or
   // fewer when there are fewer tiles.
-#define QMI_LMT(MT, NW, NS, PER_CU)                                                                   \
+#define QMI_LMT(MT, NW, NS, NSET, PER_CU)                                                             \
   do {                                                                                            \
     const int nrt = (int)((n_rows + MT - 1) / MT);                                                \
     const int64_t tiles = (int64_t)nvt * nrt;                                                     \
     const int64_t grid = std::min<int64_t>(tiles, (int64_t)device_cu_count() * PER_CU);           \
-    hipLaunchKernelGGL((lmhead_tiles<MT, NW, NS>), dim3((unsigned)grid), dim3(NW * 64), 0, s, h,   \
+    hipLaunchKernelGGL((lmhead_tiles<MT, NW, NS, NSET>), dim3((unsigned)grid), dim3(NW * 64), 0, s, \
+                       h,                                                                         \
                        h_stride, (int)n_rows, w, w_stride, (int)vocab, (int)hidden, c2, tgt,      \
                        tgt_stride, nvt, nrt, ws.part, ws.tgt_logit);                              \
   } while (0)
   if (n_rows <= 64)
-    QMI_LMT(64, 4, 3, 2);
+    QMI_LMT(64, 4, 3, QMI_LM_NSET_SMALL, 2);
   else
-    QMI_LMT(256, 8, 2, 1);
+    QMI_LMT(256, 8, 2, QMI_LM_NSET_LARGE, 1);
 #undef QMI_LMT
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? QMI_OK : (int)e;

@@ -10,6 +10,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../../include/qwen3mi.h"
 
 namespace qmi {
@@ -162,6 +164,15 @@ inline int device_cu_count() {
     cache[dev] = n;
   }
   return cache[dev];
+}
+
+// Calls f(std::integral_constant<int, i>) for i = I .. N-1.
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
 }
 
 }  // namespace qmi

@@ -143,15 +143,6 @@ __device__ __forceinline__ void lds_load16(const void* gbase, uint32_t voff, uin
                : "memory", "m0");
 }
 
-// Calls f(std::integral_constant<int, i>) for i = I .. N-1.
-template <int I, int N, class F>
-__device__ __forceinline__ void static_for(F&& f) {
-  if constexpr (I < N) {
-    f(std::integral_constant<int, I>{});
-    static_for<I + 1, N>(f);
-  }
-}
-
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
   return __builtin_bit_cast(bf16x8_t, u32x4_t{v.x, v.y, v.z, v.w});
 }
