@@ -6,13 +6,14 @@ import ctypes
 
 def test_parts_count(pkg):
     L = pkg._lib.lib()
-    # 64 rows: 64 column tiles of 16 -> split K in 4 (256 workgroups).
-    assert L.qmi_linear_rows_parts_count(64, 1024, 2048) == 4
-    assert L.qmi_linear_rows_parts_count(64, 1024, 3072) == 4
-    # 128 rows: 128 tiles of 16 columns -> 2 parts; 256 rows: tiles of 64
-    # weight rows (fewer re-reads of the activations) -> 64 tiles, 4 parts.
+    # 64 rows: 32 column tiles of 32 -> split K in 8 (256 workgroups).
+    assert L.qmi_linear_rows_parts_count(64, 1024, 2048) == 8
+    assert L.qmi_linear_rows_parts_count(64, 1024, 3072) == 8
+    # 128 rows: 128 tiles of 16 columns -> 2 parts; 256 rows: tiles of 32
+    # weight rows for K <= 2048 (128 tiles, 2 parts), of 64 above (64 tiles,
+    # 4 parts).
     assert L.qmi_linear_rows_parts_count(128, 1024, 2048) == 2
-    assert L.qmi_linear_rows_parts_count(256, 1024, 2048) == 4
+    assert L.qmi_linear_rows_parts_count(256, 1024, 2048) == 2
     assert L.qmi_linear_rows_parts_count(256, 1024, 3072) == 4
     # Never more parts than 128-element K chunks.
     assert L.qmi_linear_rows_parts_count(1, 16, 128) == 1
