@@ -55,7 +55,7 @@ EXTRA_FLAGS = {
 # Sources whose kernels place LDS waits by hand (inline-asm LDS reads with
 # explicit lgkmcnt waits, inline-asm direct global->LDS loads through M0).
 # Their device assembly is checked on every build (asm_check.py).
-ASM_CHECKED = ("varlen_prefill.hip", "linear_rows.hip")
+ASM_CHECKED = ("varlen_prefill.hip", "linear_rows.hip", "lm_head.hip")
 
 
 def hipcc_path() -> str:

@@ -10,28 +10,31 @@
 // The logits here are h . w accumulated in fp32 and never rounded, where the
 // reference rounds its lm_head output to bf16 before the fp32 softmax.
 //
-// Kernel 1, lmhead_tiles: a (128-row vocabulary tile, tile of MT hidden-state
-// rows) work item computes its logits with v_mfma_f32_16x16x32_bf16 and
-// reduces them on the spot to one (max, sum of exp2) pair per row in the log2
-// domain (x * log2(e) / T); in target mode the tile that holds a row's target
-// also writes that raw logit.  The grid is persistent (one or two workgroups
-// per CU), each workgroup running a contiguous range of work items as one
-// pipeline of (item, 64-hidden chunk) steps, so the loads never drain at item
-// boundaries.  Operands are
-// computed transposed, S^T = W H^T: A = 16 vocabulary rows x 32 hidden of W,
-// B = H^T (32 hidden x 16 rows), so both operands are 16-byte row pieces and
-// each lane's accumulators hold 4 consecutive vocabulary entries of one row.
-//   * NW waves, MT/64 per vocabulary slice: wave (vq, rq) owns vocabulary rows
-//     VW vq .. +VW of the tile (VW = 128 MT / (64 NW)) and hidden-state rows
-//     64 rq .. +64 (VW/16 x 4 MFMA tiles).
-//   * W and H are staged through registers into LDS in chunks of 64 hidden
-//     (128-byte rows), two register sets and two or three LDS stages, one
-//     barrier per chunk: the global loads of chunk k+2 are issued before
-//     chunk k is multiplied and written to LDS at the end of step k+1.  16-byte
-//     piece c of row r sits at c ^ ((r / 2) % 8): the 16 rows a 16-lane group
-//     reads then cover all 64 LDS banks.
+// Kernel 1, lmhead_items: a work item (TVB vocabulary tiles of 128 rows, a
+// tile of MT hidden-state rows) computes its logits with
+// v_mfma_f32_16x16x32_bf16 and reduces them on the spot to one (max, sum of
+// exp2) pair per row and 128-row vocabulary tile in the log2 domain
+// (x * log2(e) / T); in target mode the lane holding a row's target also
+// writes that raw logit.  The grid is persistent (one or two workgroups per
+// CU), each workgroup running a contiguous range of items as one pipeline of
+// (item, 64-hidden chunk) steps, so the loads never drain at item
+// boundaries.  Operands are computed transposed, S^T = W H^T: A = 16
+// vocabulary rows x 32 hidden of W, B = H^T (32 hidden x 16 rows), so both
+// operands are 16-byte row pieces and each lane's accumulators hold 4
+// consecutive vocabulary entries of one row.
+//   * W and H chunks go from global memory straight into LDS (gfx950
+//     global_load_lds_dwordx4, no register staging), NSTAGE stages, loads
+//     issued NSTAGE - 1 steps ahead, one wait and one barrier per step.
+//     16-byte piece c of staged row r sits at c ^ ((r / 2) % 8): the 16 rows
+//     a 16-lane group reads then cover all 64 LDS banks.
+//   * Up to 64 rows: items of 128 x 64, 4 waves of 32 vocabulary rows, three
+//     stages, two workgroups per CU.  Above: items of 256 x 256, 8 waves of
+//     128 x 64 (one wave per 128-row vocabulary tile), two 64 KB stages, one
+//     workgroup per CU: each item re-reads its hidden-state rows from L2, so
+//     256-entry items halve that traffic per FLOP (at 8,192 rows 4.07 ->
+//     2.73 ms against 128-entry items staged through registers).
 //   * W (311 MB for Qwen3-0.6B) is read once from HBM per row tile; H comes
-//     from L2.  At 256 rows the vocabulary GEMM is near the HBM / MFMA ridge.
+//     from L2.
 // Kernel 2, lmhead_sample_rows: one workgroup per row combines the row's tile
 // pairs into its log-sum-exp and draws the token by inverse transform
 // sampling with one Philox4x32-10 uniform per row: the first vocabulary index
@@ -54,14 +57,6 @@ constexpr int kKC = 64;             // hidden elements per staged chunk
 constexpr int kRowB = kKC * 2;      // bytes per staged row
 constexpr int kRowThreads = 256;    // kernel 2
 
-// Register sets of the load stream (steps of loads in flight).
-#ifndef QMI_LM_NSET_SMALL
-#define QMI_LM_NSET_SMALL 2
-#endif
-#ifndef QMI_LM_NSET_LARGE
-#define QMI_LM_NSET_LARGE 2
-#endif
-
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
   return __builtin_bit_cast(bf16x8_t, u32x4_t{v.x, v.y, v.z, v.w});
 }
@@ -69,24 +64,49 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
 // Byte offset of 16-byte piece c of staged row r.
 __device__ __forceinline__ int lds_off(int r, int c) { return r * kRowB + ((c ^ ((r >> 1) & 7)) << 4); }
 
-template <int MT, int NW, int NSTAGE, int NSET>
-__global__ __launch_bounds__(NW * 64) void lmhead_tiles(
+// Direct global -> LDS load of 16 bytes per lane (gfx950
+// global_load_lds_dwordx4): lane l's bytes at gbase + voff land at LDS byte
+// lds + 16 l.  Inline asm, so that the compiler adds no wait for it; the
+// caller waits with s_waitcnt vmcnt before the barrier that publishes the
+// stage.
+__device__ __forceinline__ void lds_load16(const void* gbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+               : : "s"(lds), "v"(voff), "s"(gbase) : "memory", "m0");
+}
+
+// Kernel 1 with larger work items and direct loads: an item is TVB
+// vocabulary tiles of 128 rows (TV = 128 TVB) x MT hidden-state rows; W and
+// H chunks go from global memory straight into NSTAGE LDS stages (no
+// register staging, no LDS write instructions), loads issued NSTAGE - 1
+// steps ahead.  Wave (vq, rq) owns vocabulary rows VW vq .. +VW (VW = 128
+// when TVB = NVQ: one wave per 128-row tile, whose (max, sum) pairs it
+// writes itself) and hidden-state rows 64 rq .. +64.  Rows past the
+// vocabulary or the batch load the last valid row (their results are
+// masked or not written).  Per-item H traffic is what bounds this kernel at
+// a few hundred rows and above (each item re-reads its MT x hidden rows from
+// L2): 256-entry items halve it per FLOP.
+template <int MT, int NW, int NSTAGE, int TVB>
+__global__ __launch_bounds__(NW * 64) void lmhead_items(
     const uint16_t* __restrict__ h, int64_t h_stride, int n_rows,
     const uint16_t* __restrict__ w, int64_t w_stride, int vocab, int hidden, float c2,
     const int64_t* __restrict__ tgt, int64_t tgt_stride, int n_vtiles, int n_rtiles,
     float2* __restrict__ part, float* __restrict__ tgt_logit) {
-  constexpr int NT = NW * 64;
+  constexpr int TV = kTV * TVB;
   constexpr int NRQ = MT / 64;       // row blocks of 64
-  constexpr int NVQ = NW / NRQ;      // waves per row block, splitting the tile's vocabulary
-  constexpr int VW = kTV / NVQ;      // vocabulary rows per wave
+  constexpr int NVQ = NW / NRQ;      // waves per row block
+  constexpr int VW = TV / NVQ;       // vocabulary rows per wave
   constexpr int VB = VW / 16;        // 16-row MFMA blocks per wave along the vocabulary
-  constexpr int W_BYTES = kTV * kRowB;
+  constexpr int WPT = kTV / VW;      // waves per 128-row vocabulary tile
+  constexpr int W_BYTES = TV * kRowB;
   constexpr int STAGE = W_BYTES + MT * kRowB;
-  constexpr int WCH = kTV * 8 / NT;  // W pieces per thread per chunk
-  constexpr int HCH = MT * 8 / NT;   // H pieces per thread per chunk
-  static_assert(NVQ * NRQ == NW && VB >= 1 && WCH >= 1 && HCH >= 1, "tile shape");
+  constexpr int WL = TV / (8 * NW);  // W wave-loads (8 rows of 128 B) per wave per chunk
+  constexpr int HL = MT / (8 * NW);  // H wave-loads per wave per chunk
+  constexpr int LPW = WL + HL;
+  static_assert(NVQ * NRQ == NW && VB >= 1 && VW <= kTV && kTV % VW == 0, "tile shape");
+  static_assert(WL >= 1 && HL >= 1 && TV % (8 * NW) == 0 && MT % (8 * NW) == 0, "loads");
+  static_assert(NSTAGE >= 2 && NSTAGE * STAGE <= 160 * 1024, "LDS");
   __shared__ __align__(16) unsigned char lds[NSTAGE * STAGE];
-  __shared__ float2 red[NVQ][MT];
+  __shared__ float2 red[WPT > 1 ? NVQ : 1][WPT > 1 ? MT : 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -94,109 +114,71 @@ __global__ __launch_bounds__(NW * 64) void lmhead_tiles(
   const int l16 = lane & 15, g4 = lane >> 4;
   const int vq = wave % NVQ, rq = wave / NVQ;
   const int n_kc = hidden / kKC;
-  // Persistent: this workgroup takes tiles [t_begin, t_end) of the
-  // vocabulary-major order (tile i = vocabulary tile i / n_rtiles, row tile
-  // i % n_rtiles, so the row tiles of one W tile run back to back and reuse
-  // it from L2), as one pipelined sequence of (tile, chunk) steps.
-  const int n_tiles = n_vtiles * n_rtiles;
-  const int t_begin = (int)((int64_t)blockIdx.x * n_tiles / gridDim.x);
-  const int t_end = (int)((int64_t)(blockIdx.x + 1) * n_tiles / gridDim.x);
-  const int n_steps = (t_end - t_begin) * n_kc;
+  const int n_vitems = (n_vtiles + TVB - 1) / TVB;
+  const int n_items = n_vitems * n_rtiles;
+  const int i_begin = (int)((int64_t)blockIdx.x * n_items / gridDim.x);
+  const int i_end = (int)((int64_t)(blockIdx.x + 1) * n_items / gridDim.x);
+  const int n_steps = (i_end - i_begin) * n_kc;
   if (n_steps == 0) return;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)lds;
 
-  // Staging: piece q = tid + i * NT of a chunk is row q / 8, piece q % 8.
-  // Loads are unconditional straight-line code (the compiler then keeps two
-  // steps of them in flight): rows past the vocabulary or the batch read the
-  // tile's last valid row, and are zeroed when the pieces are written to LDS.
-  // The load stream runs two steps ahead of the compute stream and repeats
-  // its last chunk past the end.
-  int wdst[WCH], hdst[HCH];
-#pragma unroll
-  for (int i = 0; i < WCH; ++i) {
-    const int q = tid + i * NT;
-    wdst[i] = lds_off(q >> 3, q & 7);
-  }
-#pragma unroll
-  for (int i = 0; i < HCH; ++i) {
-    const int q = tid + i * NT;
-    hdst[i] = W_BYTES + lds_off(q >> 3, q & 7);
-  }
-  uint4 wreg[NSET][WCH], hreg[NSET][HCH];
-  // Tile positions (vocabulary tile, row tile) advance incrementally: no
-  // division per step (a runtime division is a long scalar sequence, and at
-  // one instruction stream per wave it delays the MFMAs behind it).
+  // Item positions (vocabulary item, row tile) advance incrementally.
   struct Pos {
-    int vt, rt;
+    int vi, rt;
   };
-  auto advance = [&](Pos p) -> Pos { return p.rt + 1 == n_rtiles ? Pos{p.vt + 1, 0} : Pos{p.vt, p.rt + 1}; };
-  const Pos p_begin{t_begin / n_rtiles, t_begin % n_rtiles};
-  // Load stream: the next step it fetches, and the current tile's bases and
-  // per-lane element offsets (rows past the vocabulary or the batch clamped to
-  // the tile's last valid row), set up once per tile.
+  auto advance = [&](Pos p) -> Pos { return p.rt + 1 == n_rtiles ? Pos{p.vi + 1, 0} : Pos{p.vi, p.rt + 1}; };
+  const Pos p_begin{i_begin / n_rtiles, i_begin % n_rtiles};
+
+  // Load stream.  Wave-load j of this wave covers staged rows 8 (LPW' wave +
+  // j) .. +8 of W (then of H); lane l fetches row + l / 8, physical piece
+  // l % 8, i.e. logical piece (l % 8) ^ ((row / 2) % 8).
   Pos ld = p_begin;
   int ld_kc = 0, ld_step = 0;
-  const uint16_t* wt0;
-  const uint16_t* ht0;
-  int woff[WCH], hoff[HCH];
-  auto ld_tile_setup = [&]() __attribute__((always_inline)) {
-    const int v0 = ld.vt * kTV, r0 = ld.rt * MT;
-    const int wlast = min(kTV, vocab - v0) - 1;      // last valid row of the tile
+  const char* wb0;
+  const char* hb0;
+  uint32_t woff[WL], hoff[HL];
+  auto ld_item_setup = [&]() __attribute__((always_inline)) {
+    const int v0 = ld.vi * TV, r0 = ld.rt * MT;
+    const int wlast = min(TV, vocab - v0) - 1;
     const int hlast = min(MT, n_rows - r0) - 1;
-    wt0 = w + (int64_t)v0 * w_stride;
-    ht0 = h + (int64_t)r0 * h_stride;
+    wb0 = reinterpret_cast<const char*>(w + (int64_t)v0 * w_stride);
+    hb0 = reinterpret_cast<const char*>(h + (int64_t)r0 * h_stride);
 #pragma unroll
-    for (int i = 0; i < WCH; ++i) {
-      const int q = tid + i * NT;
-      woff[i] = min(q >> 3, wlast) * (int)w_stride + (q & 7) * 8;
+    for (int j = 0; j < WL; ++j) {
+      const int r = 8 * (WL * wave + j) + (lane >> 3);
+      const int c = (lane & 7) ^ ((r >> 1) & 7);
+      woff[j] = (uint32_t)((min(r, wlast) * w_stride + c * 8) * 2);
     }
 #pragma unroll
-    for (int i = 0; i < HCH; ++i) {
-      const int q = tid + i * NT;
-      hoff[i] = min(q >> 3, hlast) * (int)h_stride + (q & 7) * 8;
+    for (int j = 0; j < HL; ++j) {
+      const int r = 8 * (HL * wave + j) + (lane >> 3);
+      const int c = (lane & 7) ^ ((r >> 1) & 7);
+      hoff[j] = (uint32_t)((min(r, hlast) * h_stride + c * 8) * 2);
     }
   };
-  ld_tile_setup();
-  auto load_next = [&](auto set_c) __attribute__((always_inline)) {
-    constexpr int P = decltype(set_c)::value;
-    const uint16_t* wt = wt0 + ld_kc * kKC;
-    const uint16_t* ht = ht0 + ld_kc * kKC;
+  ld_item_setup();
+  // Issues the next step's loads into `stage` (the stream repeats its last
+  // step past the end, so every step issues the same number of loads).
+  auto issue = [&](int stage) __attribute__((always_inline)) {
+    const uint32_t sb = lds0 + stage * STAGE;
+    const char* wk = wb0 + ld_kc * kRowB;
+    const char* hk = hb0 + ld_kc * kRowB;
 #pragma unroll
-    for (int i = 0; i < WCH; ++i) wreg[P][i] = load_u4_stream(wt + woff[i]);
+    for (int j = 0; j < WL; ++j) lds_load16(wk, woff[j], sb + (WL * wave + j) * 8 * kRowB);
 #pragma unroll
-    for (int i = 0; i < HCH; ++i) hreg[P][i] = load_u4(ht + hoff[i]);
+    for (int j = 0; j < HL; ++j) lds_load16(hk, hoff[j], sb + W_BYTES + (HL * wave + j) * 8 * kRowB);
     if (ld_step + 1 < n_steps) {
       ++ld_step;
       if (++ld_kc == n_kc) {
         ld_kc = 0;
         ld = advance(ld);
-        ld_tile_setup();
+        ld_item_setup();
       }
     }
   };
-  auto store_step = [&](int stage, Pos tile, auto set_c) __attribute__((always_inline)) {
-    constexpr int P = decltype(set_c)::value;
-    unsigned char* base = lds + stage * STAGE;
-    const int wn = min(kTV, vocab - tile.vt * kTV);
-    const int hn = min(MT, n_rows - tile.rt * MT);
-#pragma unroll
-    for (int i = 0; i < WCH; ++i) {
-      const int q = tid + i * NT;
-      const uint32_t keep = (q >> 3) < wn ? 0xffffffffu : 0u;
-      const uint4 v = wreg[P][i];
-      *reinterpret_cast<uint4*>(base + wdst[i]) = make_uint4(v.x & keep, v.y & keep, v.z & keep, v.w & keep);
-    }
-#pragma unroll
-    for (int i = 0; i < HCH; ++i) {
-      const int q = tid + i * NT;
-      const uint32_t keep = (q >> 3) < hn ? 0xffffffffu : 0u;
-      const uint4 v = hreg[P][i];
-      *reinterpret_cast<uint4*>(base + hdst[i]) = make_uint4(v.x & keep, v.y & keep, v.z & keep, v.w & keep);
-    }
-  };
 
-  // Operand read offsets: row VW vq + 16 vb + l16 of W, row 64 rq + 16 rb + l16
-  // of H, piece 4 ks + g4 (hidden 32 ks + 8 g4 .. +8 of the chunk).  (r / 2) % 8
-  // of those rows is l16 / 2, so the swizzled piece does not depend on vb / rb.
+  // Operand reads: row VW vq + 16 vb + l16 of W, row 64 rq + 16 rb + l16 of
+  // H, piece 4 ks + g4; (r / 2) % 8 of those rows is l16 / 2.
   int a_off[2], b_off[2];
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
@@ -204,21 +186,15 @@ __global__ __launch_bounds__(NW * 64) void lmhead_tiles(
     a_off[ks] = (VW * vq + l16) * kRowB + pc;
     b_off[ks] = W_BYTES + (64 * rq + l16) * kRowB + pc;
   }
-
   f32x4_t acc[VB][4];
 #pragma unroll
   for (int vb = 0; vb < VB; ++vb)
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) acc[vb][rb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  // Epilogue of a tile: per row, (max, sum of exp2) over the tile's 128
-  // entries; acc[vb][rb][e] holds vocabulary v0 + VW vq + 16 vb + 4 g4 + e of
-  // row r0 + 64 rq + 16 rb + l16.
-  // Target mode: the target ids of this lane's four rows, loaded when a tile
-  // starts (straight-line loads, consumed by the tile's epilogue).
   int64_t tgt_id[4] = {-1, -1, -1, -1};
-  auto load_targets = [&](Pos tile) __attribute__((always_inline)) {
-    const int r0 = tile.rt * MT;
+  auto load_targets = [&](Pos it) __attribute__((always_inline)) {
+    const int r0 = it.rt * MT;
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
       const int row = r0 + 64 * rq + 16 * rb + l16;
@@ -226,26 +202,42 @@ __global__ __launch_bounds__(NW * 64) void lmhead_tiles(
     }
   };
 
-  auto epilogue = [&](Pos tile) __attribute__((always_inline)) {
-    const int vt = tile.vt;
-    const int64_t v0 = (int64_t)vt * kTV;
-    const int64_t r0 = (int64_t)tile.rt * MT;
+  // Epilogue of an item: per row, (max, sum of exp2) over each 128-entry
+  // vocabulary tile; acc[vb][rb][e] holds vocabulary v0 + VW vq + 16 vb +
+  // 4 g4 + e of row r0 + 64 rq + 16 rb + l16.
+  auto epilogue = [&](Pos it) __attribute__((always_inline)) {
+    const int64_t v0 = (int64_t)it.vi * TV;
+    const int64_t r0 = (int64_t)it.rt * MT;
     const int64_t vbase = v0 + VW * vq + 4 * g4;
+    const int vt = (int)(v0 / kTV) + (VW * vq) / kTV;  // this wave's 128-row tile
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
-      float x[4 * VB];
+      const int row_l = 64 * rq + 16 * rb + l16;
+      const int64_t row = r0 + row_l;
+      if (tgt && row < n_rows) {  // the raw logit of the target, by the lane holding it
+        const int64_t tl = tgt_id[rb] - vbase;  // 16 vb + e if this lane holds it
+        if (tl >= 0 && tl < VW && (tl & 12) == 0) {
+#pragma unroll
+          for (int vb = 0; vb < VB; ++vb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (tl == 16 * vb + e) tgt_logit[row] = acc[vb][rb][e];
+        }
+      }
       float mx = kNegBig;
 #pragma unroll
       for (int vb = 0; vb < VB; ++vb)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const bool ok = vbase + 16 * vb + e < vocab;
-          x[4 * vb + e] = ok ? acc[vb][rb][e] * c2 : kNegBig;
-          mx = fmaxf(mx, x[4 * vb + e]);
+          acc[vb][rb][e] = ok ? acc[vb][rb][e] * c2 : kNegBig;
+          mx = fmaxf(mx, acc[vb][rb][e]);
         }
       float sm = 0.f;
 #pragma unroll
-      for (int i = 0; i < 4 * VB; ++i) sm += fast_exp2(x[i] - mx);
+      for (int vb = 0; vb < VB; ++vb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sm += fast_exp2(acc[vb][rb][e] - mx);
       LanePair pm = lane_pair16(mx), ps = lane_pair16(sm);
       mx = pm.lo;
       sm = ps.lo;
@@ -255,48 +247,39 @@ __global__ __launch_bounds__(NW * 64) void lmhead_tiles(
       mx = pm.lo;
       sm = ps.lo;
       lse2_merge(mx, sm, pm.hi, ps.hi);
-      const int row_l = 64 * rq + 16 * rb + l16;
-      if (g4 == 0) red[vq][row_l] = make_float2(mx, sm);
-      if (tgt) {
-        const int64_t row = r0 + row_l;
-        if (row < n_rows) {
-          const int64_t tl = tgt_id[rb] - vbase;  // 16 vb + e if this lane holds it
-          if (tl >= 0 && tl < VW && (tl & 12) == 0) {
-#pragma unroll
-            for (int vb = 0; vb < VB; ++vb)
-#pragma unroll
-              for (int e = 0; e < 4; ++e)
-                if (tl == 16 * vb + e) tgt_logit[row] = acc[vb][rb][e];
-          }
-        }
+      if constexpr (WPT > 1) {
+        if (g4 == 0) red[vq][row_l] = make_float2(mx, sm);
+      } else {
+        if (g4 == 0 && row < n_rows && vt < n_vtiles) part[row * (int64_t)n_vtiles + vt] = make_float2(mx, sm);
       }
 #pragma unroll
       for (int vb = 0; vb < VB; ++vb) acc[vb][rb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
-    __syncthreads();
-    for (int r = tid; r < MT; r += NT) {
-      if (r0 + r < n_rows) {
-        float2 a = red[0][r];
+    if constexpr (WPT > 1) {
+      __syncthreads();
+      for (int r = tid; r < MT; r += NW * 64) {
+        if (r0 + r < n_rows) {
+          float2 a = red[0][r];
 #pragma unroll
-        for (int j = 1; j < NVQ; ++j) lse2_merge(a.x, a.y, red[j][r].x, red[j][r].y);
-        part[(r0 + r) * (int64_t)n_vtiles + vt] = a;
+          for (int j = 1; j < NVQ; ++j) lse2_merge(a.x, a.y, red[j][r].x, red[j][r].y);
+          part[(r0 + r) * (int64_t)n_vtiles + (int)(v0 / kTV)] = a;
+        }
       }
     }
   };
 
-  // Step st (chunk kc of tile `tile`): the loads of step st + NSET go into
-  // register set st % NSET (already in LDS), the MFMAs read stage
-  // st % NSTAGE, then set (st + 1) % NSET -- step st + 1, loaded NSET - 1
-  // steps earlier -- is written to stage (st + 1) % NSTAGE, which no wave has
-  // read since the barrier that ended step st - 1.  NSET - 1 steps of compute
-  // cover each load's latency.
-  Pos tile = p_begin;
+  // Step st: issue step st + NSTAGE - 1 into its stage (last read in step
+  // st - 1, which ended with a barrier), multiply stage st % NSTAGE, then
+  // wait for this wave's loads of step st + 1 and meet at the barrier.
+  Pos it = p_begin;
   int kc = 0, stage = 0;
-  auto step = [&](int st, auto set_c) __attribute__((always_inline)) {
-    constexpr int P = decltype(set_c)::value;
-    constexpr int PN = P + 1 == NSET ? 0 : P + 1;
-    if (tgt && kc == 0) load_targets(tile);
-    load_next(std::integral_constant<int, P>{});
+#pragma unroll
+  for (int i = 0; i < NSTAGE - 1; ++i) issue(i);
+  asm volatile("s_waitcnt vmcnt(%0)" ::"i"((NSTAGE - 2) * LPW) : "memory");
+  __syncthreads();
+  for (int st = 0; st < n_steps; ++st) {
+    if (tgt && kc == 0) load_targets(it);
+    issue(stage == 0 ? NSTAGE - 1 : stage - 1);
     const unsigned char* base = lds + stage * STAGE;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
@@ -313,24 +296,18 @@ __global__ __launch_bounds__(NW * 64) void lmhead_tiles(
         for (int rb = 0; rb < 4; ++rb)
           acc[vb][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[vb], b[rb], acc[vb][rb], 0, 0, 0);
     }
-    const int next_stage = stage == NSTAGE - 1 ? 0 : stage + 1;
-    const Pos next_tile = kc + 1 == n_kc ? advance(tile) : tile;
-    if (st + 1 < n_steps) store_step(next_stage, next_tile, std::integral_constant<int, PN>{});
+    if (kc + 1 == n_kc) {
+      epilogue(it);
+      it = advance(it);
+      kc = 0;
+    } else {
+      ++kc;
+    }
+    stage = stage + 1 == NSTAGE ? 0 : stage + 1;
+    asm volatile("s_waitcnt vmcnt(%0)" ::"i"((NSTAGE - 2) * LPW) : "memory");
     __syncthreads();
-    if (kc + 1 == n_kc) epilogue(tile);
-    stage = next_stage;
-    tile = next_tile;
-    kc = kc + 1 == n_kc ? 0 : kc + 1;
-  };
-
-  static_for<0, NSET>([&](auto i_c) __attribute__((always_inline)) { load_next(i_c); });
-  store_step(0, p_begin, std::integral_constant<int, 0>{});
-  __syncthreads();
-  for (int st = 0; st < n_steps; st += NSET) {
-    static_for<0, NSET>([&](auto i_c) __attribute__((always_inline)) {
-      if (st + (int)decltype(i_c)::value < n_steps) step(st + decltype(i_c)::value, i_c);
-    });
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 // Block-wide helpers for kernel 2 (256 threads).
@@ -553,27 +530,24 @@ int launch_tiles(const uint16_t* h, int64_t h_stride, int64_t n_rows, const uint
                  int64_t w_stride, int64_t vocab, int64_t hidden, float c2, const int64_t* tgt,
                  int64_t tgt_stride, const LmWs& ws, hipStream_t s) {
   const int nvt = (int)n_vtiles_of(vocab);
-  // Up to 64 rows: 64-row tiles, 4 waves of 32 vocabulary rows, three LDS
-  // stages, two 74 KB workgroups per CU.  Above: 256-row tiles, 8 waves of
-  // 64 x 64, two LDS stages, one 100 KB workgroup per CU (measured faster
-  // than three stages, and than 4 waves of 128 x 64 or two 128-row
-  // workgroups per CU).  A persistent grid of that many workgroups per CU, or
-  // fewer when there are fewer tiles.
-#define QMI_LMT(MT, NW, NS, NSET, PER_CU)                                                             \
+  // Up to 64 rows: items of 128 x 64, 4 waves, three LDS stages, two 74 KB
+  // workgroups per CU.  Above: items of 256 x 256, 8 waves, two LDS stages,
+  // one 128 KB workgroup per CU.  A persistent grid of that many workgroups
+  // per CU, or fewer when there are fewer items.
+#define QMI_LMI(MT, NW, NS, TVB, PER_CU)                                                              \
   do {                                                                                            \
     const int nrt = (int)((n_rows + MT - 1) / MT);                                                \
-    const int64_t tiles = (int64_t)nvt * nrt;                                                     \
-    const int64_t grid = std::min<int64_t>(tiles, (int64_t)device_cu_count() * PER_CU);           \
-    hipLaunchKernelGGL((lmhead_tiles<MT, NW, NS, NSET>), dim3((unsigned)grid), dim3(NW * 64), 0, s, \
-                       h,                                                                         \
-                       h_stride, (int)n_rows, w, w_stride, (int)vocab, (int)hidden, c2, tgt,      \
+    const int64_t items = (int64_t)((nvt + TVB - 1) / TVB) * nrt;                                 \
+    const int64_t grid = std::min<int64_t>(items, (int64_t)device_cu_count() * PER_CU);           \
+    hipLaunchKernelGGL((lmhead_items<MT, NW, NS, TVB>), dim3((unsigned)grid), dim3(NW * 64), 0, s, \
+                       h, h_stride, (int)n_rows, w, w_stride, (int)vocab, (int)hidden, c2, tgt,   \
                        tgt_stride, nvt, nrt, ws.part, ws.tgt_logit);                              \
   } while (0)
   if (n_rows <= 64)
-    QMI_LMT(64, 4, 3, QMI_LM_NSET_SMALL, 2);
+    QMI_LMI(64, 4, 3, 1, 2);
   else
-    QMI_LMT(256, 8, 2, QMI_LM_NSET_LARGE, 1);
-#undef QMI_LMT
+    QMI_LMI(256, 8, 2, 2, 1);
+#undef QMI_LMI
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? QMI_OK : (int)e;
 }
