@@ -262,27 +262,33 @@ def leg_lm_head(torch, pkg, dev, steps, warmup, vocab=151936, hidden=1024):
                    tflops=round(flops / t / 1e12, 1),
                    frac_of_bf16_mfma_peak=round(flops / t / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4))
         out[f"sample_{n}_rows"] = rec
-    # Top-k = 20 (the reference's default): materialised logits + the HIP
-    # radix-select sampler, against the reference's torch ops on the same logits.
-    n = 256
-    h = torch.randn((n, hidden), generator=g, device=dev).to(torch.bfloat16)
-    logits = h @ w.T
+    # Top-k = 20 (the reference's default), at the rollout's 256 rows and
+    # config 3's 64: the fused lm_head + top-k sampler (no logits), against
+    # the materialised bf16 logits + the HIP radix-select sampler, and the
+    # reference's torch ops on those logits.
+    for n in (64, 256):
+        h = torch.randn((n, hidden), generator=g, device=dev).to(torch.bfloat16)
+        logits = h @ w.T
 
-    def torch_topk():
-        x = logits.float() / 0.6
-        vals, idx = torch.topk(x, 20, dim=-1)
-        x = torch.full_like(x, float("-inf")).scatter(-1, idx, vals)
-        nxt = torch.multinomial(torch.softmax(x, dim=-1), num_samples=1)
-        return nxt, torch.log_softmax(x, dim=-1).gather(-1, nxt)
-    rec = {}
-    for name, fn in (("hip_sampler_us", lambda: pkg.kernels.sample_tokens_topk(logits, 20, 0.6,
+        def torch_topk():
+            x = logits.float() / 0.6
+            vals, idx = torch.topk(x, 20, dim=-1)
+            x = torch.full_like(x, float("-inf")).scatter(-1, idx, vals)
+            nxt = torch.multinomial(torch.softmax(x, dim=-1), num_samples=1)
+            return nxt, torch.log_softmax(x, dim=-1).gather(-1, nxt)
+        rec = {}
+        for name, fn in (
+                ("fused_us", lambda: pkg.kernels.lm_head_sample(h, w, 0.6, seed=1, top_k=20)),
+                ("gemm_plus_hip_sampler_us",
+                 lambda: pkg.kernels.sample_tokens_topk(h @ w.T, 20, 0.6, seed=1)),
+                ("hip_sampler_only_us", lambda: pkg.kernels.sample_tokens_topk(logits, 20, 0.6,
                                                                                seed=1)),
-                     ("torch_ops_us", torch_topk)):
-        _, per = timed_launches(torch, [fn], steps, warmup)
-        rec[name] = round(statistics.median(per) * 1e3, 2)
-    rec["rows"] = n
-    out["topk20_sampling_256_rows"] = rec
-    del logits
+                ("torch_ops_only_us", torch_topk)):
+            _, per = timed_launches(torch, [fn], steps, warmup)
+            rec[name] = round(statistics.median(per) * 1e3, 2)
+        rec["rows"] = n
+        out[f"topk20_sampling_{n}_rows"] = rec
+        del logits
     n = 8192
     h = torch.randn((n, hidden), generator=g, device=dev).to(torch.bfloat16)
     tgt = torch.randint(0, vocab, (n,), generator=g, device=dev)

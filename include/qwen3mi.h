@@ -489,37 +489,49 @@ int qmi_sample_tokens_topk(const uint16_t* logits, int64_t row_stride, int64_t n
 
 /*
  * Fused lm_head + sampling: logits = hidden_states . weight^T accumulated in
- * fp32 and never materialised, then one token per row drawn from
- * softmax(logits / temperature) with its log-probability.  Replaces
- * `logits = self.lm_head(h)` (qwen3_naive.py:1387, :1607) and, for
- * top_k = None, the sampling step of generate_continuous (:1413-1423) and
- * generate_continuous_with_logprobs (:1636-1650).
+ * fp32 and rounded to bf16 (the reference's bf16 lm_head output), never
+ * materialised; then one token per row drawn from softmax(logits / T), or,
+ * with 0 < top_k < vocab, from the softmax of the top_k largest of
+ * logits / T (the rest -inf; of entries tied at the k-th value the lowest
+ * indices are kept), with the drawn token's log-probability under that
+ * distribution.  Replaces `logits = self.lm_head(h)` (qwen3_naive.py:1387,
+ * :1607) and the sampling step of generate_continuous (:1413-1423) and
+ * generate_continuous_with_logprobs (:1636-1650), for top_k = None (pass 0)
+ * and for top_k = k <= 64 (the reference default is 20).
  * hidden_states: [n_rows, hidden] bf16 (row stride h_stride); weight:
- * [vocab, hidden] bf16 (row stride w_stride); hidden a multiple of 64,
- * pointers 16-byte aligned, strides multiples of 8.
- * Draw: inverse transform sampling -- the first vocabulary index whose
- * cumulative probability exceeds u, with u = (53 bits of words 0 and 1 of
- * Philox4x32-10 at counter (0, row, offset_lo, offset_hi), key (seed_lo,
- * seed_hi)) + 0.5, scaled by 2^-53.  A (seed, offset) pair reproduces the
- * tokens.  out_tokens int64 [n_rows]; out_logprobs fp32 [n_rows] or NULL.
- * workspace: qmi_lm_head_workspace_bytes(n_rows, vocab) bytes, 16-byte
- * aligned (per-row, per-128-entry-tile softmax pairs; no initial contents).
+ * [vocab, hidden] bf16 (row stride w_stride); hidden a multiple of 64 and at
+ * most 16384, pointers 16-byte aligned, strides multiples of 8.
+ * Draw: inverse transform sampling over the kept entries in vocabulary
+ * order -- the first index whose cumulative probability exceeds u, with
+ * u = (53 bits of words 0 and 1 of Philox4x32-10 at counter
+ * (0, lo32(q), lo32(offset) + hi32(q), hi32(offset)), key (seed_lo,
+ * seed_hi)) + 0.5, scaled by 2^-53, where q is the row's counter value:
+ * row_counters[r] (uint64 [n_rows], device memory), or r when row_counters
+ * is NULL.  Equal (seed, offset, q) reproduce a row's token, whatever the
+ * other rows.  out_tokens int64 [n_rows]; out_logprobs fp32 [n_rows] or NULL.
+ * workspace: qmi_lm_head_workspace_bytes(n_rows, vocab, top_k) bytes, 16-byte
+ * aligned (per-row, per-128-entry-tile softmax pairs and, with top-k, each
+ * tile's four largest logits; no initial contents).  top_k above 64 returns
+ * QMI_E_UNSUPPORTED (top-k sampling from materialised logits:
+ * qmi_sample_tokens_topk).
  */
-int64_t qmi_lm_head_workspace_bytes(int64_t n_rows, int64_t vocab);
+int64_t qmi_lm_head_workspace_bytes(int64_t n_rows, int64_t vocab, int64_t top_k);
 
 int qmi_lm_head_sample(const uint16_t* hidden_states, int64_t h_stride, int64_t n_rows,
                        const uint16_t* weight, int64_t w_stride, int64_t vocab, int64_t hidden,
-                       float temperature, uint64_t seed, uint64_t offset, int64_t* out_tokens,
-                       float* out_logprobs, void* workspace, int64_t workspace_bytes,
-                       void* stream);
+                       float temperature, int64_t top_k, uint64_t seed, uint64_t offset,
+                       const uint64_t* row_counters, int64_t* out_tokens, float* out_logprobs,
+                       void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * Fused lm_head + log-softmax gather: out_logprobs[r] =
- * log_softmax(hidden_states[r] . weight^T)[targets[r * target_stride]] and
- * out_lse[r] (may be NULL) its log-sum-exp, the logits fp32 and never
- * materialised.  Replaces `model(input_ids)`'s lm_head (qwen3_naive.py:826-835)
- * plus forward_logprob's gather (qwen3_grpo_train.py:46-53) for the rows
- * given.  Layout and workspace as qmi_lm_head_sample.
+ * log_softmax(bf16(hidden_states[r] . weight^T))[targets[r * target_stride]]
+ * and out_lse[r] (may be NULL) its log-sum-exp, the logits rounded to bf16 as
+ * the reference's lm_head output and never materialised.  A target outside
+ * [0, vocab) gives a NaN log-probability.  Replaces `model(input_ids)`'s
+ * lm_head (qwen3_naive.py:826-835) plus forward_logprob's gather
+ * (qwen3_grpo_train.py:46-53) for the rows given.  Layout as
+ * qmi_lm_head_sample; workspace qmi_lm_head_workspace_bytes(n_rows, vocab, 0).
  */
 int qmi_lm_head_logprob(const uint16_t* hidden_states, int64_t h_stride, int64_t n_rows,
                         const uint16_t* weight, int64_t w_stride, int64_t vocab, int64_t hidden,

@@ -78,13 +78,16 @@ def logprob_of(logits: torch.Tensor, tokens: torch.Tensor, temperature: float) -
 # sampler's draw).  Follows the same reference lines (top_k = None); the draw
 # is tok = min{i : sum_{j <= i} p_j > u}, an exact sample of Categorical(p).
 
-def uniform53(n_rows: int, seed: int, offset: int) -> np.ndarray:
+def uniform53(n_rows: int, seed: int, offset: int, row_counters=None) -> np.ndarray:
     """u[r] in (0, 1): words 0 and 1 of Philox4x32-10 at counter
-    (0, r, offset_lo, offset_hi), key (seed_lo, seed_hi), as
-    ((w0 << 21 | w1 >> 11) + 0.5) / 2^53 (float64)."""
+    (0, lo32(q_r), offset_lo + hi32(q_r) mod 2^32, offset_hi), key
+    (seed_lo, seed_hi), as ((w0 << 21 | w1 >> 11) + 0.5) / 2^53 (float64);
+    q_r = row_counters[r] (non-negative ints), or r."""
+    q = (np.arange(n_rows, dtype=np.uint64) if row_counters is None
+         else np.asarray(row_counters, dtype=np.int64).astype(np.uint64))
     ctr = np.zeros((n_rows, 4), dtype=np.uint32)
-    ctr[:, 1] = np.arange(n_rows, dtype=np.uint32)
-    ctr[:, 2] = offset & _MASK
+    ctr[:, 1] = (q & np.uint64(_MASK)).astype(np.uint32)
+    ctr[:, 2] = ((q >> np.uint64(32)) + np.uint64(offset & _MASK)) & np.uint64(_MASK)
     ctr[:, 3] = (offset >> 32) & _MASK
     w = philox4x32_10(ctr, (seed & _MASK, (seed >> 32) & _MASK))
     bits = (w[:, 0].astype(np.uint64) << np.uint64(21)) | (w[:, 1].astype(np.uint64) >> np.uint64(11))

@@ -100,10 +100,10 @@ SIGNATURES: dict[str, tuple] = {
     "qmi_sample_tokens_topk": (ctypes.c_int, [
         _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_f32, ctypes.c_uint64, ctypes.c_uint64, _c_p,
         _c_p, _c_p]),
-    "qmi_lm_head_workspace_bytes": (_c_i64, [_c_i64, _c_i64]),
+    "qmi_lm_head_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64]),
     "qmi_lm_head_sample": (ctypes.c_int, [
-        _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_f32, ctypes.c_uint64,
-        ctypes.c_uint64, _c_p, _c_p, _c_p, _c_i64, _c_p]),
+        _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_f32, _c_i64, ctypes.c_uint64,
+        ctypes.c_uint64, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_p]),
     "qmi_lm_head_logprob": (ctypes.c_int, [
         _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_p,
         _c_i64, _c_p]),

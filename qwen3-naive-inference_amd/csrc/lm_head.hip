@@ -1,27 +1,29 @@
-// Fused lm_head + softmax: token sampling with the drawn token's
-// log-probability, or the log-probabilities of given target tokens, without
-// materialising the [rows, vocab] logits.
+// Fused lm_head + softmax: token sampling (all entries, or the top k) with
+// the drawn token's log-probability, or the log-probabilities of given target
+// tokens, without materialising the [rows, vocab] logits.
 //
 // Reference semantics:
 //   qwen3_naive.py:1387 / :1607   logits = self.lm_head(h)     (h [n, 1024] bf16)
-//   qwen3_naive.py:1413-1423, :1636-1650 (top_k = None)
-//       x = logits.float() / T;  tok ~ Categorical(softmax(x));  lp = log_softmax(x)[tok]
+//   qwen3_naive.py:1413-1423, :1636-1650
+//       x = logits.float() / T;  [top_k: keep the k largest of x, the rest -inf]
+//       tok ~ Categorical(softmax(x));  lp = log_softmax(x)[tok]
 //   qwen3_grpo_train.py:46-53     lp = log_softmax(logits.float())[ids]
-// The logits here are h . w accumulated in fp32 and never rounded, where the
-// reference rounds its lm_head output to bf16 before the fp32 softmax.
+// Each logit is h . w accumulated in fp32 and rounded to bf16, as the
+// reference's bf16 lm_head output is, before the fp32 softmax.
 //
 // Kernel 1, lmhead_items: a work item (TVB vocabulary tiles of 128 rows, a
 // tile of MT hidden-state rows) computes its logits with
 // v_mfma_f32_16x16x32_bf16 and reduces them on the spot to one (max, sum of
 // exp2) pair per row and 128-row vocabulary tile in the log2 domain
 // (x * log2(e) / T); in target mode the lane holding a row's target also
-// writes that raw logit.  The grid is persistent (one or two workgroups per
-// CU), each workgroup running a contiguous range of items as one pipeline of
-// (item, 64-hidden chunk) steps, so the loads never drain at item
-// boundaries.  Operands are computed transposed, S^T = W H^T: A = 16
-// vocabulary rows x 32 hidden of W, B = H^T (32 hidden x 16 rows), so both
-// operands are 16-byte row pieces and each lane's accumulators hold 4
-// consecutive vocabulary entries of one row.
+// writes that logit; in top-k mode every (row, tile) also gets its four
+// largest logits (value descending, index ascending) as packed keys.  The
+// grid is persistent (one or two workgroups per CU), each workgroup running a
+// contiguous range of items as one pipeline of (item, 64-hidden chunk) steps,
+// so the loads never drain at item boundaries.  Operands are computed
+// transposed, S^T = W H^T: A = 16 vocabulary rows x 32 hidden of W, B = H^T
+// (32 hidden x 16 rows), so both operands are 16-byte row pieces and each
+// lane's accumulators hold 4 consecutive vocabulary entries of one row.
 //   * W and H chunks go from global memory straight into LDS (gfx950
 //     global_load_lds_dwordx4, no register staging), NSTAGE stages, loads
 //     issued NSTAGE - 1 steps ahead, one wait and one barrier per step.
@@ -39,10 +41,16 @@
 // pairs into its log-sum-exp and draws the token by inverse transform
 // sampling with one Philox4x32-10 uniform per row: the first vocabulary index
 // whose cumulative probability exceeds u (tile prefix sums in fp64, then the
-// chosen tile's 128 logits recomputed as fp32 dot products).  This is an exact
-// draw from softmax(x / T) and costs one random number per row instead of
-// one per vocabulary entry.
-// Kernel 2', lmhead_logprob_rows: lse and lp = x[target] - lse per row.
+// chosen tile's 128 logits recomputed by the same MFMA sequence as kernel 1,
+// so they are bit-identical to the values its pairs summarise).  This is an
+// exact draw from softmax(x / T) and costs one random number per row instead
+// of one per vocabulary entry.
+// Kernel 2', lmhead_topk_rows: the k kept entries are found among the
+// per-tile candidates (a radix select on their values, ties to the lowest
+// index), then drawn from by inverse transform sampling in vocabulary order.
+// The top k of a row lie in its candidates unless some tile holds four or
+// more of them; such a tile is recomputed in full and the selection repeated.
+// Kernel 2'', lmhead_logprob_rows: lse and lp = x[target] - lse per row.
 #include <algorithm>
 #include <type_traits>
 
@@ -56,9 +64,77 @@ constexpr int kTV = 128;            // vocabulary rows per tile
 constexpr int kKC = 64;             // hidden elements per staged chunk
 constexpr int kRowB = kKC * 2;      // bytes per staged row
 constexpr int kRowThreads = 256;    // kernel 2
+constexpr int kMaxFusedTopK = 64;   // largest k of the fused top-k sampler
+constexpr int kMaxHidden = 16384;
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
   return __builtin_bit_cast(bf16x8_t, u32x4_t{v.x, v.y, v.z, v.w});
+}
+
+// fp32 -> nearest bf16 (ties to even), returned as fp32: the value of the
+// reference's bf16 lm_head output.
+__device__ __forceinline__ float bf16_round(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+
+// Candidate key of a logit: the order-preserving 16-bit key of its bf16 bits
+// above the complement of its index within the 128-entry tile, so that a
+// larger key is a larger value or, for equal values, a lower index.  Key 0
+// is an empty slot (no finite logit maps to it).
+__device__ __forceinline__ uint32_t value_key16(float xr) {
+  const uint32_t b = __float_as_uint(xr) >> 16;
+  return (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
+}
+__device__ __forceinline__ uint32_t cand_key(float xr, int local) {
+  return (value_key16(xr) << 16) | (0xffffu ^ (uint32_t)local);
+}
+__device__ __forceinline__ float key_value(uint32_t key) {
+  const uint32_t k = key >> 16;
+  const uint32_t b = (k & 0x8000u) ? (k & 0x7fffu) : (~k & 0xffffu);
+  return bf16_to_f32((uint16_t)b);
+}
+__device__ __forceinline__ int key_local(uint32_t key) { return (int)((key & 0xffffu) ^ 0xffffu); }
+
+__device__ __forceinline__ uint32_t umed3(uint32_t a, uint32_t b, uint32_t c) {
+  return max(min(a, b), min(max(a, b), c));  // v_med3_u32
+}
+
+// The four largest keys, c0 > c1 > c2 > c3 (0 = empty).  Inserting x keeps
+// the four largest of the five: with the list sorted, max(c_i, min(c_{i-1}, x))
+// is med3(c_{i-1}, c_i, x).
+struct Top4 {
+  uint32_t c0, c1, c2, c3;
+  __device__ __forceinline__ void insert(uint32_t x) {
+    const uint32_t n3 = umed3(c2, c3, x), n2 = umed3(c1, c2, x), n1 = umed3(c0, c1, x);
+    c0 = max(c0, x);
+    c1 = n1;
+    c2 = n2;
+    c3 = n3;
+  }
+  // Adds another list whose keys are distinct from this one's.
+  __device__ __forceinline__ void merge(const Top4& o) {
+    insert(o.c0);
+    insert(o.c1);
+    insert(o.c2);
+    insert(o.c3);
+  }
+};
+
+// The union of the lists of lanes l and l ^ XOR (XOR = 16 or 32), identical
+// on both lanes: the lane swaps hand every lane the pair's two lists, which
+// are merged from empty in the same order on both sides.
+template <int XOR>
+__device__ __forceinline__ Top4 top4_pair_union(const Top4& t) {
+  uint32_t lo[4], hi[4];
+  const uint32_t v[4] = {t.c0, t.c1, t.c2, t.c3};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const auto r = XOR == 16 ? __builtin_amdgcn_permlane16_swap(v[i], v[i], false, false)
+                             : __builtin_amdgcn_permlane32_swap(v[i], v[i], false, false);
+    lo[i] = r[0];
+    hi[i] = r[1];
+  }
+  Top4 u{lo[0], lo[1], lo[2], lo[3]};
+  u.merge(Top4{hi[0], hi[1], hi[2], hi[3]});
+  return u;
 }
 
 // Byte offset of 16-byte piece c of staged row r.
@@ -84,13 +160,14 @@ __device__ __forceinline__ void lds_load16(const void* gbase, uint32_t voff, uin
 // vocabulary or the batch load the last valid row (their results are
 // masked or not written).  Per-item H traffic is what bounds this kernel at
 // a few hundred rows and above (each item re-reads its MT x hidden rows from
-// L2): 256-entry items halve it per FLOP.
-template <int MT, int NW, int NSTAGE, int TVB>
+// L2): 256-entry items halve it per FLOP.  TOPK also writes each (row, tile)'s
+// four largest logits as candidate keys (cand[row * n_vtiles + tile]).
+template <int MT, int NW, int NSTAGE, int TVB, bool TOPK>
 __global__ __launch_bounds__(NW * 64) void lmhead_items(
     const uint16_t* __restrict__ h, int64_t h_stride, int n_rows,
     const uint16_t* __restrict__ w, int64_t w_stride, int vocab, int hidden, float c2,
     const int64_t* __restrict__ tgt, int64_t tgt_stride, int n_vtiles, int n_rtiles,
-    float2* __restrict__ part, float* __restrict__ tgt_logit) {
+    float2* __restrict__ part, float* __restrict__ tgt_logit, uint4* __restrict__ cand) {
   constexpr int TV = kTV * TVB;
   constexpr int NRQ = MT / 64;       // row blocks of 64
   constexpr int NVQ = NW / NRQ;      // waves per row block
@@ -107,6 +184,7 @@ __global__ __launch_bounds__(NW * 64) void lmhead_items(
   static_assert(NSTAGE >= 2 && NSTAGE * STAGE <= 160 * 1024, "LDS");
   __shared__ __align__(16) unsigned char lds[NSTAGE * STAGE];
   __shared__ float2 red[WPT > 1 ? NVQ : 1][WPT > 1 ? MT : 1];
+  __shared__ uint4 redk[WPT > 1 && TOPK ? NVQ : 1][WPT > 1 && TOPK ? MT : 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -204,17 +282,23 @@ __global__ __launch_bounds__(NW * 64) void lmhead_items(
 
   // Epilogue of an item: per row, (max, sum of exp2) over each 128-entry
   // vocabulary tile; acc[vb][rb][e] holds vocabulary v0 + VW vq + 16 vb +
-  // 4 g4 + e of row r0 + 64 rq + 16 rb + l16.
+  // 4 g4 + e of row r0 + 64 rq + 16 rb + l16.  Each logit is first rounded
+  // to bf16 (the reference's lm_head output).
   auto epilogue = [&](Pos it) __attribute__((always_inline)) {
     const int64_t v0 = (int64_t)it.vi * TV;
     const int64_t r0 = (int64_t)it.rt * MT;
     const int64_t vbase = v0 + VW * vq + 4 * g4;
     const int vt = (int)(v0 / kTV) + (VW * vq) / kTV;  // this wave's 128-row tile
+    const int lbase = (VW * vq) % kTV + 4 * g4;        // its first entry within the tile
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
       const int row_l = 64 * rq + 16 * rb + l16;
       const int64_t row = r0 + row_l;
-      if (tgt && row < n_rows) {  // the raw logit of the target, by the lane holding it
+#pragma unroll
+      for (int vb = 0; vb < VB; ++vb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[vb][rb][e] = bf16_round(acc[vb][rb][e]);
+      if (tgt && row < n_rows) {  // the target's logit, by the lane holding it
         const int64_t tl = tgt_id[rb] - vbase;  // 16 vb + e if this lane holds it
         if (tl >= 0 && tl < VW && (tl & 12) == 0) {
 #pragma unroll
@@ -222,6 +306,22 @@ __global__ __launch_bounds__(NW * 64) void lmhead_items(
 #pragma unroll
             for (int e = 0; e < 4; ++e)
               if (tl == 16 * vb + e) tgt_logit[row] = acc[vb][rb][e];
+        }
+      }
+      if constexpr (TOPK) {
+        Top4 t{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int vb = 0; vb < VB; ++vb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (vbase + 16 * vb + e < vocab) t.insert(cand_key(acc[vb][rb][e], lbase + 16 * vb + e));
+        t = top4_pair_union<16>(t);
+        t = top4_pair_union<32>(t);
+        if constexpr (WPT > 1) {
+          if (g4 == 0) redk[vq][row_l] = make_uint4(t.c0, t.c1, t.c2, t.c3);
+        } else {
+          if (g4 == 0 && row < n_rows && vt < n_vtiles)
+            cand[row * (int64_t)n_vtiles + vt] = make_uint4(t.c0, t.c1, t.c2, t.c3);
         }
       }
       float mx = kNegBig;
@@ -263,6 +363,16 @@ __global__ __launch_bounds__(NW * 64) void lmhead_items(
 #pragma unroll
           for (int j = 1; j < NVQ; ++j) lse2_merge(a.x, a.y, red[j][r].x, red[j][r].y);
           part[(r0 + r) * (int64_t)n_vtiles + (int)(v0 / kTV)] = a;
+          if constexpr (TOPK) {
+            const uint4 k0 = redk[0][r];
+            Top4 t{k0.x, k0.y, k0.z, k0.w};
+#pragma unroll
+            for (int j = 1; j < NVQ; ++j) {
+              const uint4 kj = redk[j][r];
+              t.merge(Top4{kj.x, kj.y, kj.z, kj.w});
+            }
+            cand[(r0 + r) * (int64_t)n_vtiles + (int)(v0 / kTV)] = make_uint4(t.c0, t.c1, t.c2, t.c3);
+          }
         }
       }
     }
@@ -368,32 +478,82 @@ __device__ RowLse row_lse(const float2* __restrict__ pr, int n, int cpt, double*
   return {m2, total};
 }
 
+// The Philox4x32-10 uniform of a row: u in (0, 1) with 53 bits from words 0
+// and 1 of the block at counter (0, lo32(q), lo32(offset) + hi32(q),
+// hi32(offset)), key (seed_lo, seed_hi), where q is the row's 64-bit counter
+// value (row_ctr[row], or the row index when row_ctr is NULL).
+__device__ __forceinline__ double row_uniform(int row, const uint64_t* __restrict__ row_ctr,
+                                              uint32_t seed_lo, uint32_t seed_hi, uint32_t off_lo,
+                                              uint32_t off_hi) {
+  const uint64_t q = row_ctr ? row_ctr[row] : (uint64_t)row;
+  const uint4 r = philox4x32_10(make_uint4(0u, (uint32_t)q, off_lo + (uint32_t)(q >> 32), off_hi),
+                                seed_lo, seed_hi);
+  const uint64_t bits = ((uint64_t)r.x << 21) | (uint64_t)(r.y >> 11);
+  return ((double)bits + 0.5) * 0x1p-53;
+}
+
+// Copies a hidden-state row into LDS (read by tile_logits).
+__device__ __forceinline__ void load_hrow(const uint16_t* __restrict__ hr, int hidden,
+                                          uint16_t* hrow) {
+  for (int k = 8 * (int)threadIdx.x; k < hidden; k += 8 * kRowThreads)
+    *reinterpret_cast<uint4*>(hrow + k) = load_u4(hr + k);
+}
+
+// The bf16-rounded logits of vocabulary tile `tile` (entries 128 tile .. +128)
+// for the hidden-state row in LDS, into xs[128] (-inf past the vocabulary).
+// All 256 threads take part; wave i computes entries 32 i .. +32 with the
+// MFMA sequence of lmhead_items (the same operand layout, hidden elements in
+// the same order: 32 at a time, lane group g4 supplying elements 8 g4 .. +8
+// of each 32), every column of the B operand holding the row, so the values
+// are bit-identical to the ones lmhead_items reduced.
+__device__ void tile_logits(const uint16_t* hrow, const uint16_t* __restrict__ w,
+                            int64_t w_stride, int vocab, int hidden, int tile, float* xs) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l16 = lane & 15, g4 = lane >> 4;
+  const int64_t vw = (int64_t)tile * kTV + 32 * wave;
+  const uint16_t* wr0 = w + (vw + l16 < vocab ? vw + l16 : (int64_t)vocab - 1) * w_stride + 8 * g4;
+  const uint16_t* wr1 = w + (vw + 16 + l16 < vocab ? vw + 16 + l16 : (int64_t)vocab - 1) * w_stride + 8 * g4;
+  f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+  for (int k = 0; k < hidden; k += 64) {  // hidden is a multiple of 64
+    const uint4 a00 = load_u4(wr0 + k), a10 = load_u4(wr1 + k);
+    const uint4 a01 = load_u4(wr0 + k + 32), a11 = load_u4(wr1 + k + 32);
+    const bf16x8_t b0 = as_bf16x8(*reinterpret_cast<const uint4*>(hrow + k + 8 * g4));
+    const bf16x8_t b1 = as_bf16x8(*reinterpret_cast<const uint4*>(hrow + k + 32 + 8 * g4));
+    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a00), b0, acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a10), b0, acc1, 0, 0, 0);
+    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a01), b1, acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a11), b1, acc1, 0, 0, 0);
+  }
+  if (l16 == 0) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int64_t v0 = vw + 4 * g4 + e, v1 = v0 + 16;
+      xs[32 * wave + 4 * g4 + e] = v0 < vocab ? bf16_round(acc0[e]) : -INFINITY;
+      xs[32 * wave + 16 + 4 * g4 + e] = v1 < vocab ? bf16_round(acc1[e]) : -INFINITY;
+    }
+  }
+}
+
 __global__ __launch_bounds__(kRowThreads) void lmhead_sample_rows(
     const float2* __restrict__ part, int n_vtiles, const uint16_t* __restrict__ h,
     int64_t h_stride, const uint16_t* __restrict__ w, int64_t w_stride, int vocab, int hidden,
     float c2, uint32_t seed_lo, uint32_t seed_hi, uint32_t off_lo, uint32_t off_hi,
-    int64_t* __restrict__ out_tok, float* __restrict__ out_lp) {
+    const uint64_t* __restrict__ row_ctr, int64_t* __restrict__ out_tok, float* __restrict__ out_lp) {
   __shared__ float smf[4];
   __shared__ double smd[5];
   __shared__ float xs[kTV];
   __shared__ int sel_tile;
   __shared__ double sel_resid;
-  __shared__ __align__(16) uint16_t hrow[16384];
+  __shared__ __align__(16) uint16_t hrow[kMaxHidden];
   const int tid = threadIdx.x;
   const int row = blockIdx.x;
   const float2* pr = part + (int64_t)row * n_vtiles;
-  const uint16_t* hr = h + (int64_t)row * h_stride;
-  // The row's hidden state into LDS (read by every column below).
-  for (int k = 8 * tid; k < hidden; k += 8 * kRowThreads)
-    *reinterpret_cast<uint4*>(hrow + k) = load_u4(hr + k);
+  load_hrow(h + (int64_t)row * h_stride, hidden, hrow);
   const int cpt = (n_vtiles + kRowThreads - 1) / kRowThreads;
   double own, excl;
   const RowLse L = row_lse(pr, n_vtiles, cpt, &own, &excl, smf, smd);
 
-  // u in (0, 1) with 53 bits from the first two words of the row's block.
-  const uint4 r = philox4x32_10(make_uint4(0u, (uint32_t)row, off_lo, off_hi), seed_lo, seed_hi);
-  const uint64_t bits = ((uint64_t)r.x << 21) | (uint64_t)(r.y >> 11);
-  const double u = ((double)bits + 0.5) * 0x1p-53;
+  const double u = row_uniform(row, row_ctr, seed_lo, seed_hi, off_lo, off_hi);
   const double target = u * L.s;
 
   if (tid == 0) {
@@ -425,28 +585,7 @@ __global__ __launch_bounds__(kRowThreads) void lmhead_sample_rows(
     __syncthreads();
   }
   const int t_sel = sel_tile;
-
-  // The chosen tile's logits for this row: thread t takes column t / 2 and
-  // half t % 2 of the hidden dimension (all loads of a thread independent).
-  {
-    const int c = tid >> 1, half = tid & 1;
-    const int64_t v = (int64_t)t_sel * kTV + c;
-    float d = 0.f;
-    if (v < vocab) {
-      const uint16_t* wr = w + v * w_stride;
-      const int k0 = half * (hidden / 2), k1 = k0 + hidden / 2;
-#pragma unroll 8
-      for (int k = k0; k < k1; k += 8) {
-        const uint4 a = *reinterpret_cast<const uint4*>(hrow + k), b = load_u4(wr + k);
-        d = dot2_bf16(a.x, b.x, d);
-        d = dot2_bf16(a.y, b.y, d);
-        d = dot2_bf16(a.z, b.z, d);
-        d = dot2_bf16(a.w, b.w, d);
-      }
-    }
-    d += __shfl_xor(d, 1, 64);
-    if (half == 0) xs[c] = v < vocab ? d : -INFINITY;
-  }
+  tile_logits(hrow, w, w_stride, vocab, hidden, t_sel, xs);
   __syncthreads();
   // Within the tile: the first column whose cumulative mass exceeds the
   // residual (wave 0, two columns per lane, fixed-order scan).
@@ -471,15 +610,274 @@ __global__ __launch_bounds__(kRowThreads) void lmhead_sample_rows(
       out_tok[row] = (int64_t)t_sel * kTV + pick;
       if (out_lp) {
         const double lse2 = (double)L.m2 + log2(L.s);
-        out_lp[row] = (float)(((double)xs[pick] * (double)c2 - lse2) * (double)kLn2);
+        out_lp[row] = (float)(((double)(xs[pick] * c2) - lse2) * (double)kLn2);
       }
+    }
+  }
+}
+
+// Exclusive prefix (fixed order) of one int per thread over the 256 threads;
+// also returns the total.  sm holds 4 ints.
+__device__ int block_excl_scan_i32(int x, int* sm, int* total) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  int inc = x;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(inc, d, 64);
+    if (lane >= d) inc += y;
+  }
+  __syncthreads();
+  if (lane == 63) sm[wv] = inc;
+  __syncthreads();
+  int base = 0;
+  for (int j = 0; j < wv; ++j) base += sm[j];
+  *total = sm[0] + sm[1] + sm[2] + sm[3];
+  return base + inc - x;
+}
+
+// Top-k sampling from the per-(row, tile) candidates of lmhead_items (TOPK).
+// The kept set is the k largest logits, ties at the k-th value kept in
+// vocabulary order (lowest indices first).  Every entry of the kept set
+// outside a tile's four candidates would need four larger ones in the same
+// tile: a tile whose fourth candidate is kept ("saturated", at most k / 4 of
+// them) is recomputed in full (tile_logits) and the selection repeated over
+// the tiles' candidates with those tiles' 128 logits in place of their four;
+// adding entries only raises the k-th value, so no further tile saturates.
+// One 256-lane workgroup per row; thread t owns the contiguous tiles
+// [t cpt, t cpt + cpt), which keeps every scan in vocabulary order.
+__global__ __launch_bounds__(kRowThreads) void lmhead_topk_rows(
+    const uint4* __restrict__ cand, int n_vtiles, const uint16_t* __restrict__ h, int64_t h_stride,
+    const uint16_t* __restrict__ w, int64_t w_stride, int vocab, int hidden, int k, float c2,
+    uint32_t seed_lo, uint32_t seed_hi, uint32_t off_lo, uint32_t off_hi,
+    const uint64_t* __restrict__ row_ctr, int64_t* __restrict__ out_tok, float* __restrict__ out_lp) {
+  constexpr int kMaxSat = kMaxFusedTopK / 4;
+  __shared__ uint32_t hist[256];
+  __shared__ int sel[3];  // threshold value key, entries above it, equal ones kept
+  __shared__ int smi[4];
+  __shared__ double smd[5];
+  __shared__ float smf[4];
+  __shared__ int n_sat;
+  __shared__ int sat_tile[kMaxSat];
+  __shared__ float sat_x[kMaxSat][kTV];
+  __shared__ int kept_idx[kMaxFusedTopK];
+  __shared__ float kept_x[kMaxFusedTopK];  // logit * c2
+  __shared__ int pick_sm;
+  __shared__ __align__(16) uint16_t hrow[kMaxHidden];
+  const int tid = threadIdx.x;
+  const int row = blockIdx.x;
+  const uint4* cr = cand + (int64_t)row * n_vtiles;
+  const int cpt = (n_vtiles + kRowThreads - 1) / kRowThreads;
+  const int lo = min(n_vtiles, tid * cpt), hi = min(n_vtiles, lo + cpt);
+  if (tid == 0) n_sat = 0;
+
+  // The candidates of tile t in descending key order (equal values in
+  // vocabulary order): the expanded tile's 128 logits in index order carry
+  // the same keys, so both forms feed f(key, vocabulary index).
+  auto slot_of = [&](int t) {
+    const int ns = min(n_sat, kMaxSat);
+    for (int j = 0; j < ns; ++j)
+      if (sat_tile[j] == t) return j;
+    return -1;
+  };
+  auto for_each = [&](auto&& f) {
+    for (int t = lo; t < hi; ++t) {
+      const int sl = slot_of(t);
+      if (sl >= 0) {
+        for (int j = 0; j < kTV; ++j) {
+          const float x = sat_x[sl][j];
+          if (x != -INFINITY) f(cand_key(x, j), t * kTV + j);
+        }
+      } else {
+        const uint4 c = cr[t];
+        const uint32_t kk[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (kk[j]) f(kk[j], t * kTV + key_local(kk[j]));
+      }
+    }
+  };
+  // Radix select of the k-th largest value key (16 bits, high byte then low
+  // byte); sel = {threshold, entries above it, entries equal to it that are
+  // kept}.  Fewer than k entries in all: threshold 0, every entry kept.
+  auto select = [&]() {
+    hist[tid] = 0;
+    __syncthreads();
+    for_each([&](uint32_t key, int) { atomicAdd(&hist[key >> 24], 1u); });
+    __syncthreads();
+    if (tid == 0) {
+      int cum = 0, b = 255;
+      for (; b >= 0; --b) {
+        if (cum + (int)hist[b] >= k) break;
+        cum += (int)hist[b];
+      }
+      sel[0] = b;     // high byte, or -1 when everything is kept
+      sel[1] = cum;
+    }
+    __syncthreads();
+    const int hb = sel[0];
+    if (hb < 0) {
+      __syncthreads();
+      if (tid == 0) {
+        sel[0] = 0;
+        sel[2] = 0;
+      }
+      __syncthreads();
+      return;
+    }
+    hist[tid] = 0;
+    __syncthreads();
+    for_each([&](uint32_t key, int) {
+      if ((int)(key >> 24) == hb) atomicAdd(&hist[(key >> 16) & 0xffu], 1u);
+    });
+    __syncthreads();
+    if (tid == 0) {
+      int cum = sel[1], b = 255;
+      for (; b > 0; --b) {
+        if (cum + (int)hist[b] >= k) break;
+        cum += (int)hist[b];
+      }
+      sel[0] = (hb << 8) | b;
+      sel[1] = cum;
+      sel[2] = k - cum;
+    }
+    __syncthreads();
+  };
+
+  // Pass 1 over the four candidates per tile.
+  __syncthreads();
+  select();
+  {
+    const uint32_t tk = (uint32_t)sel[0];
+    const int need_eq = sel[2];
+    int eq = 0;
+    for_each([&](uint32_t key, int) { eq += (key >> 16) == tk; });
+    int tot;
+    int eq_at = block_excl_scan_i32(eq, smi, &tot);
+    for (int t = lo; t < hi; ++t) {
+      const uint4 c = cr[t];
+      const uint32_t kk[4] = {c.x, c.y, c.z, c.w};
+      bool kept3 = false;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t v = kk[j] >> 16;
+        const bool kept = kk[j] && (v > tk || (v == tk && eq_at < need_eq));
+        if (kk[j] && v == tk) ++eq_at;
+        if (j == 3) kept3 = kept;
+      }
+      if (kept3) {
+        const int sl = atomicAdd(&n_sat, 1);
+        if (sl < kMaxSat) sat_tile[sl] = t;
+      }
+    }
+  }
+  __syncthreads();
+  const int ns = min(n_sat, kMaxSat);
+  if (ns > 0) {
+    // Saturated tiles: all 128 logits, then the selection once more.
+    load_hrow(h + (int64_t)row * h_stride, hidden, hrow);
+    __syncthreads();
+    for (int j = 0; j < ns; ++j) tile_logits(hrow, w, w_stride, vocab, hidden, sat_tile[j], sat_x[j]);
+    __syncthreads();
+    select();
+  }
+
+  // The kept entries, gathered in vocabulary order.
+  const uint32_t tk = (uint32_t)sel[0];
+  const int need_eq = sel[2];
+  int gt = 0, eq = 0;
+  for_each([&](uint32_t key, int) {
+    gt += (key >> 16) > tk;
+    eq += (key >> 16) == tk;
+  });
+  int tot;
+  const int eq_before = block_excl_scan_i32(eq, smi, &tot);
+  const int take = max(0, min(eq, need_eq - eq_before));
+  int pos = block_excl_scan_i32(gt + take, smi, &tot);
+  const int nk = tot;  // k, or every entry when there are fewer
+  {
+    int taken = 0;
+    for (int t = lo; t < hi; ++t) {
+      // Kept entries of tile t in index order: at most 3 of the four
+      // candidates of a tile that did not saturate, any of an expanded one.
+      int ki[4];
+      float kx[4];
+      int nkt = 0;
+      const int sl = slot_of(t);
+      if (sl >= 0) {
+        for (int j = 0; j < kTV; ++j) {
+          const float x = sat_x[sl][j];
+          if (x == -INFINITY) continue;
+          const uint32_t v = value_key16(x);
+          const bool keep = v > tk || (v == tk && taken < take);
+          if (v == tk && keep) ++taken;
+          if (keep) {
+            kept_idx[pos] = t * kTV + j;
+            kept_x[pos] = x * c2;
+            ++pos;
+          }
+        }
+        continue;
+      }
+      const uint4 c = cr[t];
+      const uint32_t kk[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t v = kk[j] >> 16;
+        const bool keep = kk[j] && (v > tk || (v == tk && taken < take));
+        if (kk[j] && v == tk && keep) ++taken;
+        if (keep) {
+          ki[nkt] = t * kTV + key_local(kk[j]);
+          kx[nkt] = key_value(kk[j]);
+          ++nkt;
+        }
+      }
+      // Insertion sort by index (value order -> vocabulary order).
+      for (int a = 1; a < nkt; ++a)
+        for (int b = a; b > 0 && ki[b - 1] > ki[b]; --b) {
+          const int ti = ki[b];
+          ki[b] = ki[b - 1];
+          ki[b - 1] = ti;
+          const float tx = kx[b];
+          kx[b] = kx[b - 1];
+          kx[b - 1] = tx;
+        }
+      for (int a = 0; a < nkt; ++a) {
+        kept_idx[pos] = ki[a];
+        kept_x[pos] = kx[a] * c2;
+        ++pos;
+      }
+    }
+  }
+  __syncthreads();
+
+  // Inverse transform sampling over the kept entries (x c2, rounded once when
+  // stored, so that every use below sees the same value) in vocabulary order.
+  float mx = kNegBig;
+  for (int j = tid; j < nk; j += kRowThreads) mx = fmaxf(mx, kept_x[j]);
+  const float m2 = block_max256(mx, smf);
+  double p = 0.0;
+  if (tid < nk) p = (double)fast_exp2(kept_x[tid] - m2);
+  double s_tot;
+  const double excl = block_excl_scan256(p, smd, &s_tot);
+  const double target = row_uniform(row, row_ctr, seed_lo, seed_hi, off_lo, off_hi) * s_tot;
+  if (tid == 0) pick_sm = nk - 1;  // u * S rounded up to S: the last entry
+  __syncthreads();
+  if (tid < nk && p > 0.0 && target >= excl && target < excl + p) pick_sm = tid;
+  __syncthreads();
+  if (tid == 0) {
+    const int j = pick_sm;
+    out_tok[row] = kept_idx[j];
+    if (out_lp) {
+      const double lse2 = (double)m2 + log2(s_tot);
+      out_lp[row] = (float)(((double)kept_x[j] - lse2) * (double)kLn2);
     }
   }
 }
 
 __global__ __launch_bounds__(kRowThreads) void lmhead_logprob_rows(
     const float2* __restrict__ part, int n_vtiles, const float* __restrict__ tgt_logit,
-    float c2, float* __restrict__ out_lp, float* __restrict__ out_lse) {
+    const int64_t* __restrict__ tgt, int64_t tgt_stride, int vocab, float c2,
+    float* __restrict__ out_lp, float* __restrict__ out_lse) {
   __shared__ float smf[4];
   __shared__ double smd[5];
   const int row = blockIdx.x;
@@ -489,7 +887,12 @@ __global__ __launch_bounds__(kRowThreads) void lmhead_logprob_rows(
   if (threadIdx.x == 0) {
     const double lse = ((double)L.m2 + log2(L.s)) * (double)kLn2;  // of x * c2 / log2(e)
     if (out_lse) out_lse[row] = (float)lse;
-    out_lp[row] = (float)((double)tgt_logit[row] * (double)c2 * (double)kLn2 - lse);
+    const int64_t t = tgt[(int64_t)row * tgt_stride];
+    // A target outside the vocabulary has no logit: NaN (the reference's
+    // gather would raise).
+    out_lp[row] = (t < 0 || t >= vocab)
+                      ? __builtin_nanf("")
+                      : (float)((double)tgt_logit[row] * (double)c2 * (double)kLn2 - lse);
   }
 }
 
@@ -498,55 +901,71 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 struct LmWs {
   float2* part;
   float* tgt_logit;
+  uint4* cand;
 };
 
 inline int64_t n_vtiles_of(int64_t vocab) { return (vocab + kTV - 1) / kTV; }
+inline int64_t round256(int64_t b) { return (b + 255) & ~(int64_t)255; }
 
-inline int64_t ws_bytes(int64_t n_rows, int64_t vocab) {
-  const int64_t p = n_rows * n_vtiles_of(vocab) * (int64_t)sizeof(float2);
-  return ((p + 255) & ~(int64_t)255) + n_rows * (int64_t)sizeof(float);
+// Workspace: (max, sum) pairs [rows, tiles] fp32x2, target logits [rows]
+// fp32, then with top-k the candidate keys [rows, tiles] uint32x4.
+inline int64_t ws_bytes(int64_t n_rows, int64_t vocab, bool topk) {
+  const int64_t nt = n_vtiles_of(vocab);
+  const int64_t b = round256(n_rows * nt * (int64_t)sizeof(float2)) + round256(n_rows * (int64_t)sizeof(float));
+  return topk ? b + n_rows * nt * (int64_t)sizeof(uint4) : b;
 }
 
 inline LmWs ws_layout(void* ws, int64_t n_rows, int64_t vocab) {
-  const int64_t p = n_rows * n_vtiles_of(vocab) * (int64_t)sizeof(float2);
+  const int64_t nt = n_vtiles_of(vocab);
+  const int64_t p = round256(n_rows * nt * (int64_t)sizeof(float2));
+  const int64_t t = round256(n_rows * (int64_t)sizeof(float));
   char* base = static_cast<char*>(ws);
-  return {reinterpret_cast<float2*>(base), reinterpret_cast<float*>(base + ((p + 255) & ~(int64_t)255))};
+  return {reinterpret_cast<float2*>(base), reinterpret_cast<float*>(base + p),
+          reinterpret_cast<uint4*>(base + p + t)};
 }
 
 int check_args(const uint16_t* h, int64_t h_stride, int64_t n_rows, const uint16_t* w,
-               int64_t w_stride, int64_t vocab, int64_t hidden, void* ws, int64_t ws_size) {
+               int64_t w_stride, int64_t vocab, int64_t hidden, void* ws, int64_t ws_size,
+               bool topk) {
   if (n_rows < 0 || vocab <= 0 || hidden <= 0) return QMI_E_BAD_SHAPE;
   if (!h || !w || !ws) return QMI_E_NULL_POINTER;
-  if (hidden % kKC != 0 || hidden > 16384) return QMI_E_UNSUPPORTED;
+  if (hidden % kKC != 0 || hidden > kMaxHidden) return QMI_E_UNSUPPORTED;
   if (vocab > 0x7fffffffLL - kTV || n_rows > 0x7fffffffLL) return QMI_E_UNSUPPORTED;
   if (h_stride < hidden || w_stride < hidden) return QMI_E_BAD_STRIDE;
   if (h_stride % 8 || w_stride % 8 || !aligned16(h) || !aligned16(w) || !aligned16(ws))
     return QMI_E_BAD_STRIDE;
-  if (ws_size < ws_bytes(n_rows, vocab)) return QMI_E_WORKSPACE_TOO_SMALL;
+  if (ws_size < ws_bytes(n_rows, vocab, topk)) return QMI_E_WORKSPACE_TOO_SMALL;
   return QMI_OK;
 }
 
 int launch_tiles(const uint16_t* h, int64_t h_stride, int64_t n_rows, const uint16_t* w,
                  int64_t w_stride, int64_t vocab, int64_t hidden, float c2, const int64_t* tgt,
-                 int64_t tgt_stride, const LmWs& ws, hipStream_t s) {
+                 int64_t tgt_stride, bool topk, const LmWs& ws, hipStream_t s) {
   const int nvt = (int)n_vtiles_of(vocab);
   // Up to 64 rows: items of 128 x 64, 4 waves, three LDS stages, two 74 KB
   // workgroups per CU.  Above: items of 256 x 256, 8 waves, two LDS stages,
   // one 128 KB workgroup per CU.  A persistent grid of that many workgroups
   // per CU, or fewer when there are fewer items.
-#define QMI_LMI(MT, NW, NS, TVB, PER_CU)                                                              \
+#define QMI_LMI(MT, NW, NS, TVB, PER_CU, TOPK)                                                     \
   do {                                                                                            \
     const int nrt = (int)((n_rows + MT - 1) / MT);                                                \
     const int64_t items = (int64_t)((nvt + TVB - 1) / TVB) * nrt;                                 \
     const int64_t grid = std::min<int64_t>(items, (int64_t)device_cu_count() * PER_CU);           \
-    hipLaunchKernelGGL((lmhead_items<MT, NW, NS, TVB>), dim3((unsigned)grid), dim3(NW * 64), 0, s, \
-                       h, h_stride, (int)n_rows, w, w_stride, (int)vocab, (int)hidden, c2, tgt,   \
-                       tgt_stride, nvt, nrt, ws.part, ws.tgt_logit);                              \
+    hipLaunchKernelGGL((lmhead_items<MT, NW, NS, TVB, TOPK>), dim3((unsigned)grid), dim3(NW * 64), \
+                       0, s, h, h_stride, (int)n_rows, w, w_stride, (int)vocab, (int)hidden, c2,  \
+                       tgt, tgt_stride, nvt, nrt, ws.part, ws.tgt_logit, ws.cand);                \
   } while (0)
-  if (n_rows <= 64)
-    QMI_LMI(64, 4, 3, 1, 2);
-  else
-    QMI_LMI(256, 8, 2, 2, 1);
+  if (n_rows <= 64) {
+    if (topk)
+      QMI_LMI(64, 4, 3, 1, 2, true);
+    else
+      QMI_LMI(64, 4, 3, 1, 2, false);
+  } else {
+    if (topk)
+      QMI_LMI(256, 8, 2, 2, 1, true);
+    else
+      QMI_LMI(256, 8, 2, 2, 1, false);
+  }
 #undef QMI_LMI
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? QMI_OK : (int)e;
@@ -554,19 +973,22 @@ int launch_tiles(const uint16_t* h, int64_t h_stride, int64_t n_rows, const uint
 
 }  // namespace
 
-extern "C" int64_t qmi_lm_head_workspace_bytes(int64_t n_rows, int64_t vocab) {
+extern "C" int64_t qmi_lm_head_workspace_bytes(int64_t n_rows, int64_t vocab, int64_t top_k) {
   if (n_rows <= 0 || vocab <= 0) return 0;
-  return ws_bytes(n_rows, vocab);
+  return ws_bytes(n_rows, vocab, top_k > 0 && top_k < vocab);
 }
 
 extern "C" int qmi_lm_head_sample(const uint16_t* hidden_states, int64_t h_stride, int64_t n_rows,
                                   const uint16_t* weight, int64_t w_stride, int64_t vocab,
-                                  int64_t hidden, float temperature, uint64_t seed,
-                                  uint64_t offset, int64_t* out_tokens, float* out_logprobs,
-                                  void* workspace, int64_t workspace_bytes, void* stream) {
+                                  int64_t hidden, float temperature, int64_t top_k, uint64_t seed,
+                                  uint64_t offset, const uint64_t* row_counters,
+                                  int64_t* out_tokens, float* out_logprobs, void* workspace,
+                                  int64_t workspace_bytes, void* stream) {
+  if (top_k < 0 || top_k > kMaxFusedTopK) return QMI_E_UNSUPPORTED;
   if (n_rows == 0 && vocab > 0 && hidden > 0) return QMI_OK;
+  const bool topk = top_k > 0 && top_k < vocab;  // k >= vocab keeps every entry
   int st = check_args(hidden_states, h_stride, n_rows, weight, w_stride, vocab, hidden, workspace,
-                      workspace_bytes);
+                      workspace_bytes, topk);
   if (st != QMI_OK) return st;
   if (!out_tokens) return QMI_E_NULL_POINTER;
   if (!(temperature > 0.f) || temperature == INFINITY) return QMI_E_BAD_SHAPE;
@@ -574,12 +996,20 @@ extern "C" int qmi_lm_head_sample(const uint16_t* hidden_states, int64_t h_strid
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const LmWs ws = ws_layout(workspace, n_rows, vocab);
   st = launch_tiles(hidden_states, h_stride, n_rows, weight, w_stride, vocab, hidden, c2, nullptr,
-                    0, ws, s);
+                    0, topk, ws, s);
   if (st != QMI_OK) return st;
-  hipLaunchKernelGGL(lmhead_sample_rows, dim3((unsigned)n_rows), dim3(kRowThreads), 0, s, ws.part,
-                     (int)n_vtiles_of(vocab), hidden_states, h_stride, weight, w_stride, (int)vocab,
-                     (int)hidden, c2, (uint32_t)seed, (uint32_t)(seed >> 32), (uint32_t)offset,
-                     (uint32_t)(offset >> 32), out_tokens, out_logprobs);
+  if (topk)
+    hipLaunchKernelGGL(lmhead_topk_rows, dim3((unsigned)n_rows), dim3(kRowThreads), 0, s, ws.cand,
+                       (int)n_vtiles_of(vocab), hidden_states, h_stride, weight, w_stride,
+                       (int)vocab, (int)hidden, (int)top_k, c2, (uint32_t)seed,
+                       (uint32_t)(seed >> 32), (uint32_t)offset, (uint32_t)(offset >> 32),
+                       row_counters, out_tokens, out_logprobs);
+  else
+    hipLaunchKernelGGL(lmhead_sample_rows, dim3((unsigned)n_rows), dim3(kRowThreads), 0, s,
+                       ws.part, (int)n_vtiles_of(vocab), hidden_states, h_stride, weight, w_stride,
+                       (int)vocab, (int)hidden, c2, (uint32_t)seed, (uint32_t)(seed >> 32),
+                       (uint32_t)offset, (uint32_t)(offset >> 32), row_counters, out_tokens,
+                       out_logprobs);
   QMI_RETURN_LAUNCH_STATUS();
 }
 
@@ -590,15 +1020,16 @@ extern "C" int qmi_lm_head_logprob(const uint16_t* hidden_states, int64_t h_stri
                                    int64_t workspace_bytes, void* stream) {
   if (n_rows == 0 && vocab > 0 && hidden > 0) return QMI_OK;
   int st = check_args(hidden_states, h_stride, n_rows, weight, w_stride, vocab, hidden, workspace,
-                      workspace_bytes);
+                      workspace_bytes, false);
   if (st != QMI_OK) return st;
   if (!targets || !out_logprobs) return QMI_E_NULL_POINTER;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const LmWs ws = ws_layout(workspace, n_rows, vocab);
   st = launch_tiles(hidden_states, h_stride, n_rows, weight, w_stride, vocab, hidden, kLog2e,
-                    targets, target_stride, ws, s);
+                    targets, target_stride, false, ws, s);
   if (st != QMI_OK) return st;
   hipLaunchKernelGGL(lmhead_logprob_rows, dim3((unsigned)n_rows), dim3(kRowThreads), 0, s, ws.part,
-                     (int)n_vtiles_of(vocab), ws.tgt_logit, kLog2e, out_logprobs, out_lse);
+                     (int)n_vtiles_of(vocab), ws.tgt_logit, targets, target_stride, (int)vocab,
+                     kLog2e, out_logprobs, out_lse);
   QMI_RETURN_LAUNCH_STATUS();
 }

@@ -234,25 +234,28 @@ def paged_decode_attention_qkv(qkv: torch.Tensor, q_norm_weight: torch.Tensor,
 # ---------------------------------------------------------------------------
 # Varlen paged causal prefill (flash_attn_varlen_func at qwen3_naive.py:631-637)
 # ---------------------------------------------------------------------------
-# Per-device prefill workspace.  Its first bytes hold the work-queue counters
-# of the attention kernel, which must be zero before a launch and are left
-# zero by every launch, so it is zero-filled once when (re)allocated and then
-# reused; launches that share it run in stream order (torch's current stream).
-_PREFILL_WS: dict[int, torch.Tensor] = {}
+# Prefill workspaces.  The first bytes of a workspace hold the work-queue
+# counters of the attention kernel, which must be zero before a launch and
+# are left zero by every launch: a buffer is zero-filled when allocated and
+# then reused.  Eager calls reuse one buffer per (device, stream) -- calls on
+# one stream run in stream order, calls on two streams never share counters
+# -- and a larger problem gets a new buffer (the old one is released in
+# stream order by the caching allocator).  Under graph capture every call
+# gets a zero-filled buffer of its own from the graph's memory pool: the
+# captured fill re-zeroes it on each replay, and no eager call can resize or
+# free memory a graph replays into.
+_PREFILL_WS: dict[tuple[int, int], torch.Tensor] = {}
 
 
 def _prefill_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    n = (nbytes + 3) // 4
     if torch.cuda.is_current_stream_capturing():
-        cached = _PREFILL_WS.get(device.index)
-        if cached is not None and cached.numel() * 4 >= nbytes:
-            return cached
-        # A buffer made during capture belongs to the graph's pool: zero-filled
-        # by a captured fill kernel on every replay, never cached.
-        return torch.zeros((nbytes + 3) // 4, dtype=torch.float32, device=device)
-    ws = _PREFILL_WS.get(device.index)
-    if ws is None or ws.numel() * 4 < nbytes:
-        ws = torch.zeros((nbytes + 3) // 4, dtype=torch.float32, device=device)
-        _PREFILL_WS[device.index] = ws
+        return torch.zeros(n, dtype=torch.float32, device=device)
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    ws = _PREFILL_WS.get(key)
+    if ws is None or ws.numel() < n:
+        ws = torch.zeros(n, dtype=torch.float32, device=device)
+        _PREFILL_WS[key] = ws
     return ws
 
 
@@ -281,7 +284,8 @@ def varlen_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: to
     ``split_keys > 0`` forces pieces of that many keys.  ``workspace``
     (float32, at least ``qmi_varlen_prefill_workspace_bytes`` bytes, zeroed
     before its first use and left zeroed by every call) defaults to one
-    cached per device.
+    cached per (device, stream), or a fresh one per call under graph
+    capture.
     """
     if not causal:
         raise ValueError("only causal=True is supported (the reference always passes it)")
@@ -365,6 +369,9 @@ def _rows2d(name: str, x: torch.Tensor) -> torch.Tensor:
     if x2.stride(1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
         x2 = _dense16(x2)
     return x2
+
+
+NORM_MAX_WIDTH = 4096  # widest row the RMSNorm kernels take (128 lanes x 4 x 8 bf16)
 
 
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
@@ -697,59 +704,79 @@ def sample_tokens_topk(logits: torch.Tensor, top_k: int, temperature: float = 1.
     return tok, lp
 
 
-def _lm_head_args(hidden: torch.Tensor, weight: torch.Tensor):
+MAX_FUSED_TOP_K = 64  # largest k the fused lm_head top-k sampler takes
+
+
+def _lm_head_args(hidden: torch.Tensor, weight: torch.Tensor, top_k: int = 0):
     for n, t in (("hidden", hidden), ("weight", weight)):
         _require_cuda(n, t)
         _require_dtype(n, t, torch.bfloat16)
     if hidden.dim() != 2 or weight.dim() != 2 or hidden.shape[1] != weight.shape[1]:
         raise ValueError(f"hidden [N, H] and weight [V, H] must share H, got {tuple(hidden.shape)} "
                          f"and {tuple(weight.shape)}")
-    if hidden.shape[1] % 64:
-        raise ValueError(f"hidden size must be a multiple of 64, got {hidden.shape[1]}")
+    if hidden.shape[1] % 64 or hidden.shape[1] > 16384:
+        raise ValueError(f"hidden size must be a multiple of 64 and at most 16384, got "
+                         f"{hidden.shape[1]}")
     if weight.stride(1) != 1 or weight.stride(0) % 8 or weight.data_ptr() % 16:
         raise ValueError("weight rows must be contiguous, 16-byte aligned, stride % 8 == 0")
     if hidden.stride(1) != 1 or hidden.stride(0) % 8 or hidden.data_ptr() % 16:
         hidden = hidden.contiguous()
     n, hdim = hidden.shape
     v = weight.shape[0]
-    nbytes = lib().qmi_lm_head_workspace_bytes(n, v)
+    nbytes = lib().qmi_lm_head_workspace_bytes(n, v, int(top_k))
     ws = torch.empty((max(nbytes, 16) + 15) // 16 * 16, dtype=torch.uint8, device=hidden.device)
     return hidden, n, v, hdim, ws
 
 
 def lm_head_sample(hidden: torch.Tensor, weight: torch.Tensor, temperature: float = 1.0,
-                   seed: int | None = None, offset: int = 0, want_logprobs: bool = True):
-    """``logits = hidden @ weight.T`` (fp32, never materialised), then one token
-    per row drawn from ``softmax(logits / temperature)`` and its log-probability
-    (qwen3_naive.py:1387 / :1607 lm_head, :1413-1423 / :1636-1650 sampling,
-    top_k = None).  Returns ``(tokens int64 [N], logprobs fp32 [N] or None)``.
+                   seed: int | None = None, offset: int = 0, want_logprobs: bool = True,
+                   top_k: int | None = None, row_counters: torch.Tensor | None = None):
+    """``logits = bf16(hidden @ weight.T)`` (never materialised), then one token
+    per row drawn from ``softmax(logits / temperature)`` -- or, with ``top_k``,
+    from the softmax of its ``top_k`` largest entries (ties at the k-th value
+    keep the lowest indices) -- and its log-probability under that
+    distribution (qwen3_naive.py:1387 / :1607 lm_head, :1413-1423 /
+    :1636-1650 sampling).  ``top_k`` up to ``MAX_FUSED_TOP_K``.  Returns
+    ``(tokens int64 [N], logprobs fp32 [N] or None)``.
 
     The draw is inverse transform sampling with one Philox4x32-10 uniform per
-    row (counter (0, row, offset), key seed); ``seed`` defaults to a draw from
-    torch's default CPU generator, so ``torch.manual_seed`` makes the tokens
-    reproducible."""
+    row: counter (0, lo32(q), lo32(offset) + hi32(q), hi32(offset)), key seed,
+    where q is ``row_counters[r]`` (int64 ``[N]`` on the device) or the row
+    index.  ``seed`` defaults to a draw from torch's default CPU generator, so
+    ``torch.manual_seed`` makes the tokens reproducible."""
     if not (temperature > 0.0) or temperature == float("inf"):
         raise ValueError(f"temperature must be finite and > 0, got {temperature}")
-    hidden, n, v, hdim, ws = _lm_head_args(hidden, weight)
+    k = 0 if top_k is None else int(top_k)
+    if not 0 <= k <= MAX_FUSED_TOP_K:
+        raise ValueError(f"top_k must be None or in [1, {MAX_FUSED_TOP_K}], got {top_k}")
+    hidden, n, v, hdim, ws = _lm_head_args(hidden, weight, k)
     if seed is None:
         seed = int(torch.randint(0, 2 ** 62, (1,)).item())
     tok = torch.empty((n,), dtype=torch.int64, device=hidden.device)
     lp = torch.empty((n,), dtype=torch.float32, device=hidden.device) if want_logprobs else None
     if n == 0:
         return tok, lp
+    rc = None
+    if row_counters is not None:
+        _require_cuda("row_counters", row_counters)
+        _require_dtype("row_counters", row_counters, torch.int64)
+        if row_counters.shape != (n,):
+            raise ValueError(f"row_counters must be [{n}], got {tuple(row_counters.shape)}")
+        rc = row_counters.contiguous()
     st = lib().qmi_lm_head_sample(hidden.data_ptr(), hidden.stride(0), n, weight.data_ptr(),
-                                  weight.stride(0), v, hdim, float(temperature),
+                                  weight.stride(0), v, hdim, float(temperature), k,
                                   int(seed) & (2 ** 64 - 1), int(offset) & (2 ** 64 - 1),
-                                  tok.data_ptr(), _ptr(lp), ws.data_ptr(), ws.numel(),
+                                  _ptr(rc), tok.data_ptr(), _ptr(lp), ws.data_ptr(), ws.numel(),
                                   stream_handle(hidden.device))
     check(st, "lm_head_sample")
     return tok, lp
 
 
 def lm_head_logprob(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Tensor):
-    """``log_softmax(hidden @ weight.T)[targets]`` per row without materialising
-    the logits (lm_head + qwen3_grpo_train.py:46-53's gather).  ``targets``:
-    int64 ``[N]``.  Returns ``(logprobs fp32 [N], lse fp32 [N])``."""
+    """``log_softmax(bf16(hidden @ weight.T))[targets]`` per row without
+    materialising the logits (lm_head + qwen3_grpo_train.py:46-53's gather).
+    ``targets``: int64 ``[N]``; a target outside the vocabulary gives NaN.
+    Returns ``(logprobs fp32 [N], lse fp32 [N])``."""
     hidden, n, v, hdim, ws = _lm_head_args(hidden, weight)
     _require_cuda("targets", targets)
     tg = targets.reshape(-1).to(torch.int64)

@@ -89,8 +89,9 @@ def forward_logprob(model, input_ids):
     as the reference gathers position t's logits at token t).
 
     Without autograd the lm_head and the gather run fused (``lm_head_logprob``:
-    fp32 logits, never materialised); with autograd the bf16 logits are
-    materialised and the gather has a HIP backward."""
+    the logits rounded to bf16 as the lm_head's output is, never
+    materialised); with autograd the bf16 logits are materialised and the
+    gather has a HIP backward."""
     weight = getattr(getattr(model, "lm_head", None), "weight", None)
     if (not torch.is_grad_enabled() and weight is not None and weight.is_cuda
             and weight.dtype == torch.bfloat16 and hasattr(model, "model")):

@@ -83,7 +83,9 @@ def _decode_linear(proj: nn.Linear, x: torch.Tensor, parts: bool = False):
     + RMSNorm that follows sums them), else ``proj(x)``."""
     w = proj.weight
     if proj.bias is None and _use_kernels(x, w) and K.linear_rows_ok(x, w):
-        return K.linear_rows_parts(x, w) if parts else K.linear_rows(x, w)
+        if parts and w.shape[0] <= K.NORM_MAX_WIDTH:  # the norm that sums them takes the width
+            return K.linear_rows_parts(x, w)
+        return K.linear_rows(x, w)
     return proj(x)
 
 
@@ -109,7 +111,8 @@ class RMSNorm(nn.Module):
                 x = x.dense()
             else:
                 return K.add_rms_norm_parts(x, residual, self.weight, self.eps)
-        if x.dtype != torch.bfloat16 or not _use_kernels(x, self.weight):
+        if (x.dtype != torch.bfloat16 or x.shape[-1] > K.NORM_MAX_WIDTH
+                or not _use_kernels(x, self.weight)):
             return self._torch(x, residual)
         if residual is None:
             return K.rms_norm(x, self.weight, self.eps)
@@ -512,7 +515,7 @@ class Qwen3ForCausalLM(nn.Module):
                         self._graph_pool = graph.pool()
                     (self._graphs_units if pps else self._graphs)[bs] = graph
             self._has_cuda_graphs = True
-        except Exception as e:  # pragma: no cover - depends on the runtime
+        except Exception as e:
             print(f"HIP graph capture failed, decoding eagerly: {e}")
             self._graphs = {}
             self._graphs_units = {}
@@ -657,24 +660,27 @@ class Qwen3ForCausalLM(nn.Module):
             budget -= seq.num_scheduled_tokens
         return scheduled
 
-    def _sample(self, h, temperature, top_k, want_logprobs):
+    def _sample(self, h, temperature, top_k, want_logprobs, row_counters=None, seed=None):
         """lm_head + temperature / top-k / softmax / multinomial (qwen3_naive.py:1387,
         :1413-1423) and, optionally, the sampled tokens' log-probabilities
         (:1649-1650), from the final hidden states ``h`` of the sampled rows.
 
-        Without top-k the fused HIP kernel computes the logits in fp32 inside
-        the sampler (they are never materialised) and draws each token by
-        inverse transform sampling with one Philox uniform per row, seeded from
-        torch's CPU generator; with top-k the bf16 logits are materialised and
-        a HIP radix-select sampler keeps the k largest and draws among them."""
+        The fused HIP kernel rounds the logits to bf16 as the reference's
+        lm_head output, keeps them out of memory, and draws each token by
+        inverse transform sampling with one Philox uniform per row, from all
+        entries (top_k None) or from the top k (k <= 64, the reference default
+        20); ``row_counters`` (int64 per row) key each row's uniform, else the
+        row index does.  Larger k samples from materialised bf16 logits with a
+        HIP radix-select sampler."""
         w = self.lm_head.weight
         if top_k is not None and top_k >= w.shape[0]:
             top_k = None  # keeping every entry is plain sampling
         kern = h.dtype == torch.bfloat16 and h.is_cuda and w.dtype == torch.bfloat16
-        if top_k is None and kern:
-            return K.lm_head_sample(h, w, temperature, want_logprobs=want_logprobs)
+        if kern and (top_k is None or top_k <= K.MAX_FUSED_TOP_K):
+            return K.lm_head_sample(h, w, temperature, seed=seed, want_logprobs=want_logprobs,
+                                    top_k=top_k, row_counters=row_counters)
         if kern and top_k <= 1024:
-            return K.sample_tokens_topk(self.lm_head(h), top_k, temperature,
+            return K.sample_tokens_topk(self.lm_head(h), top_k, temperature, seed=seed,
                                         want_logprobs=want_logprobs)
         x = self.lm_head(h).float()
         if temperature != 1.0:
@@ -685,6 +691,17 @@ class Qwen3ForCausalLM(nn.Module):
         nxt = torch.multinomial(torch.softmax(x, dim=-1), num_samples=1)
         lp = torch.log_softmax(x, dim=-1).gather(-1, nxt)[:, 0] if want_logprobs else None
         return nxt[:, 0], lp
+
+    def _row_counters(self, seqs):
+        """Per-row Philox counter values (j << 32) | i for the j-th generated
+        token of the call's i-th sequence: a token's random number depends on
+        the call's seed, its sequence and its position only, not on the batch
+        it is sampled in (lookahead, preemption and EOS retirement leave the
+        draws of the other sequences unchanged)."""
+        q = np.fromiter(((s.num_completion_tokens << 32) | s.seq_index for s in seqs),
+                        dtype=np.int64, count=len(seqs))
+        host = torch.from_numpy(q).pin_memory()
+        return host.to(self._device(), non_blocking=True)
 
     @torch.no_grad()
     def _generate(self, prompt_ids_list, max_new_tokens, temperature, top_k, eos_token_ids,
@@ -699,17 +716,30 @@ class Qwen3ForCausalLM(nn.Module):
         waiting = deque(Sequence(p, {"temperature": temperature, "max_tokens": max_new_tokens})
                         for p in prompts)
         all_seqs = list(waiting)
+        for i, s in enumerate(all_seqs):
+            s.seq_index = i
+        seed = int(torch.randint(0, 2 ** 62, (1,)).item())  # one per call (torch.manual_seed)
         running: list[Sequence] = []
         self._preemptions = 0
         self.last_stats = {"steps": 0, "decode_steps": 0, "graph_steps": 0, "unit_graph_steps": 0,
-                           "lookahead_steps": 0}
+                           "lookahead_steps": 0, "eos_finished": 0, "discarded_rows": 0}
         dev = self._device()
-        # Decode lookahead: without EOS a sequence finishes by count alone, so
-        # the host can launch decode step t+1 (its input ids gathered on the
-        # device from step t's samples) before it reads step t's tokens back;
-        # step t's tokens then fill placeholders while step t+1 runs.
-        lookahead = eos is None and self.decode_lookahead
+        # Decode lookahead: the host launches decode step t+1 (its input ids
+        # gathered on the device from step t's samples) before it reads step
+        # t's tokens back; step t's tokens then fill placeholders while step
+        # t+1 runs.  A sequence that drew an EOS token at step t is retired
+        # when the tokens arrive: its row of step t+1 is discarded (its token
+        # dropped, its pages freed; the next step is ordered after it on the
+        # stream).
+        lookahead = self.decode_lookahead
         pending = None
+
+        def finish(s):
+            s.status = "FINISHED"
+            bm.deallocate(s.block_table)
+            s.block_table.clear()
+            if s in running:
+                running.remove(s)
 
         def flush():
             nonlocal pending
@@ -719,13 +749,16 @@ class Qwen3ForCausalLM(nn.Module):
             toks = pending["tok_host"].tolist()
             lps = pending["lp_host"].tolist() if pending["lp_host"] is not None else None
             for j, (s, at) in enumerate(pending["seqs"]):
-                if at >= len(s.token_ids) or s.token_ids[at] != _PENDING_TOKEN:
-                    continue  # preempted since (its tokens were rolled back)
+                if at is None or at >= len(s.token_ids) or s.token_ids[at] != _PENDING_TOKEN:
+                    continue  # retired, or preempted since (its tokens were rolled back)
                 s.token_ids[at] = toks[j]
                 if at == len(s.token_ids) - 1:
                     s.last_token = toks[j]
                 if lps is not None:
                     s.response_log_probs.append(lps[j])
+                if eos is not None and toks[j] in eos and s.status != "FINISHED":
+                    self.last_stats["eos_finished"] += 1
+                    finish(s)
             pending = None
 
         while waiting or running:
@@ -747,6 +780,9 @@ class Qwen3ForCausalLM(nn.Module):
                            for s in scheduled]
                     if min(idx) < 0:
                         flush()
+                        scheduled = self._drop_finished(scheduled)
+                        if not scheduled:
+                            continue
                     elif idx == list(range(pending["n"])):
                         ids_dev = pending["tok_dev"]
                     else:
@@ -754,6 +790,7 @@ class Qwen3ForCausalLM(nn.Module):
                 self.last_stats["decode_steps"] += 1
                 if ids_dev is not None:
                     self.last_stats["lookahead_steps"] += 1
+                rc = self._row_counters(scheduled)
                 h = None
                 if use_graphs and self._has_cuda_graphs:
                     h = self._run_decode_graph_seqs(scheduled, ids_dev)
@@ -764,7 +801,7 @@ class Qwen3ForCausalLM(nn.Module):
                     if ids_dev is not None:
                         ids = ids_dev
                     h = self.model.forward_decode(ids, pos, ctx, bt, slots)
-                nxt, lp = self._sample(h, temperature, top_k, with_logprobs)
+                nxt, lp = self._sample(h, temperature, top_k, with_logprobs, rc, seed)
                 n = len(scheduled)
                 tok_host = torch.empty((n,), dtype=torch.int64, pin_memory=True)
                 tok_host.copy_(nxt, non_blocking=True)
@@ -775,22 +812,29 @@ class Qwen3ForCausalLM(nn.Module):
                 event = torch.cuda.Event()
                 event.record()
                 flush()  # the previous step's tokens, while this step runs
+                rows_at = []
                 for s in scheduled:
+                    s.num_scheduled_tokens = 0
+                    if s.status == "FINISHED":  # drew EOS last step: this row is discarded
+                        self.last_stats["discarded_rows"] += 1
+                        rows_at.append((s, None))
+                        continue
                     s.kv_len += 1
                     s.append_token(_PENDING_TOKEN)
-                    s.num_scheduled_tokens = 0
-                pending = {"seqs": [(s, len(s.token_ids) - 1) for s in scheduled],
-                           "row_of": {id(s): j for j, s in enumerate(scheduled)}, "n": n,
-                           "tok_dev": nxt, "tok_host": tok_host, "lp_host": lp_host,
+                    rows_at.append((s, len(s.token_ids) - 1))
+                pending = {"seqs": rows_at, "row_of": {id(s): j for j, s in enumerate(scheduled)},
+                           "n": n, "tok_dev": nxt, "tok_host": tok_host, "lp_host": lp_host,
                            "event": event}
                 for s in scheduled:
-                    if s.num_completion_tokens >= s.max_tokens:
-                        s.status = "FINISHED"
-                        bm.deallocate(s.block_table)
-                        s.block_table.clear()
-                        running.remove(s)
+                    if s.status != "FINISHED" and s.num_completion_tokens >= s.max_tokens:
+                        finish(s)
                 continue
-            flush()
+            if pending is not None:
+                flush()
+                scheduled = self._drop_finished(scheduled)
+                if not scheduled:
+                    continue
+                all_decode = all(s.num_scheduled_tokens == 1 for s in scheduled)
             if all_decode:
                 self.last_stats["decode_steps"] += 1
                 h = None
@@ -819,25 +863,38 @@ class Qwen3ForCausalLM(nn.Module):
                     s.num_scheduled_tokens = 0
                 continue
             hs = h if sample_idx is None else h[torch.tensor(sample_idx, device=h.device)]
-            nxt, lp = self._sample(hs, temperature, top_k, with_logprobs)
+            sampled = [s for s in scheduled if s.num_scheduled_tokens == 1 or s.kv_len >= s.num_prompt_tokens]
+            nxt, lp = self._sample(hs, temperature, top_k, with_logprobs,
+                                   self._row_counters(sampled), seed)
             toks = nxt.tolist()
             lps = lp.tolist() if lp is not None else None
-            sampled = [s for s in scheduled if s.num_scheduled_tokens == 1 or s.kv_len >= s.num_prompt_tokens]
             for j, s in enumerate(sampled):
                 tok = toks[j]
                 s.append_token(tok)
                 if lps is not None:
                     s.response_log_probs.append(lps[j])
-                if (eos is not None and tok in eos) or s.num_completion_tokens >= s.max_tokens:
-                    s.status = "FINISHED"
-                    bm.deallocate(s.block_table)
-                    s.block_table.clear()
-                    running.remove(s)
+                if eos is not None and tok in eos:
+                    self.last_stats["eos_finished"] += 1
+                    finish(s)
+                elif s.num_completion_tokens >= s.max_tokens:
+                    finish(s)
             for s in scheduled:
                 s.num_scheduled_tokens = 0
         flush()
         self.last_stats["preemptions"] = self._preemptions
+        self.last_stats["blocks_in_use"] = self._num_blocks - bm.available
         return all_seqs
+
+    @staticmethod
+    def _drop_finished(scheduled):
+        """The scheduled sequences minus those an EOS token just retired."""
+        out = []
+        for s in scheduled:
+            if s.status == "FINISHED":
+                s.num_scheduled_tokens = 0
+            else:
+                out.append(s)
+        return out
 
     def generate_continuous(self, prompt_ids_list, max_new_tokens=256, temperature=0.6, top_k=20,
                             eos_token_ids=None, use_graphs=True):

@@ -4,6 +4,7 @@ chunked / prefix-cache / decode self-consistency the reference's own tests
 assert (top-1 equal, top-20 overlap)."""
 import sys
 
+import numpy as np
 import pytest
 import torch
 
@@ -222,14 +223,21 @@ def test_graph_decode_whole_units(pkg, model, monkeypatch):
     model._graphs_units = {}
 
 
-def _oracle_logprobs(model, toks, plen, n_layers=LAYERS, mode="fp32"):
+def _oracle_logprobs(model, toks, plen, n_layers=LAYERS, mode="fp32", top_k=None,
+                     temperature=1.0):
     """Oracle log-probabilities of the generated tokens toks[plen:], each
-    scored at the previous position (temperature 1, no top-k: the sampling
-    distribution of generate_continuous_with_logprobs, qwen3_naive.py:1636-1650)."""
+    scored at the previous position under the sampling distribution of
+    generate_continuous_with_logprobs (qwen3_naive.py:1636-1650): logits / T,
+    restricted to the top k when top_k is given."""
+    from oracle import sampling as OS
     logits = OM.qwen3_logits(model.state_dict(), torch.as_tensor(toks[:-1])[None], n_layers,
                              mode=mode)[0]
-    lp = torch.log_softmax(logits.double(), -1)
     tgt = torch.as_tensor(toks[plen:])
+    if top_k is None:
+        lp = torch.log_softmax(logits.double() / temperature, -1)
+    else:
+        lp = OS.topk_logprobs(logits[plen - 1:].float(), top_k, temperature)
+        return lp.gather(-1, tgt[:, None])[:, 0]
     return lp[plen - 1:].gather(-1, tgt[:, None])[:, 0]
 
 
@@ -244,14 +252,15 @@ LP_BF16_MAX, LP_BF16_MEAN = 0.12, 0.03
 LP_FP32_MAX, LP_FP32_MEAN = 0.12, 0.035
 
 
-def _assert_logprobs_match_oracle(model, toks, lps, plens, n_layers=LAYERS, rows=None, tag=""):
+def _assert_logprobs_match_oracle(model, toks, lps, plens, n_layers=LAYERS, rows=None, tag="",
+                                  top_k=None, temperature=1.0):
     """Engine log-probs against the oracle teacher-forced on the engine's own
     tokens, in both oracle modes."""
     d16, d32 = [], []
     for b in (range(len(toks)) if rows is None else rows):
         got = torch.tensor(lps[b], dtype=torch.float64)
         for mode, acc in (("bf16", d16), ("fp32", d32)):
-            ref = _oracle_logprobs(model, toks[b], plens[b], n_layers, mode)
+            ref = _oracle_logprobs(model, toks[b], plens[b], n_layers, mode, top_k, temperature)
             assert got.shape == ref.shape
             acc.append((got - ref).abs())
     d16, d32 = torch.cat(d16), torch.cat(d32)
@@ -388,3 +397,183 @@ def test_lookahead_readmitted_victim(pkg, model, prompt_len):
     prompts = [torch.randint(0, VOCAB, (1, prompt_len), generator=g) for _ in range(2)]
     new_tokens = 600 - prompt_len
     _lookahead_vs_sync(model, prompts, new_tokens, True, 5, oracle_rows=[1])
+
+
+EOS_IDS = list(range(3, VOCAB, 16))   # 128 of 2,048 ids: ~6% of the mass per step
+
+
+def _check_eos_retirement(gen, lps, new_tokens):
+    """A sequence ends at its first EOS token, else after new_tokens."""
+    early = 0
+    for g_, l_ in zip(gen, lps):
+        assert len(l_) == len(g_)
+        hits = [j for j, t in enumerate(g_) if t in EOS_IDS]
+        if hits:
+            assert hits[0] == len(g_) - 1, (hits, len(g_))
+            early += len(g_) < new_tokens
+        else:
+            assert len(g_) == new_tokens
+    return early
+
+
+@pytest.mark.parametrize("lookahead", [False, True])
+def test_eos_rollout_retires_sequences(pkg, model, lookahead):
+    """EOS-terminated rollout (qwen3_naive.py:1430-1466, :1656-1668): a
+    sequence that draws an EOS token is retired at once (its pages freed, no
+    token after the EOS), the others continue; log-probs match the oracle
+    teacher-forced on the engine's tokens.  With the decode lookahead the step
+    launched before the EOS was read back carries the retired row, whose token
+    is discarded."""
+    g = torch.Generator().manual_seed(40)
+    prompts = [torch.randint(0, VOCAB, (1, n), generator=g) for n in (30, 250, 64, 257, 5, 120,
+                                                                       300, 77)]
+    model.decode_lookahead = lookahead
+    try:
+        torch.manual_seed(11)
+        print(f"[model] EOS rollout lookahead={lookahead}", flush=True)
+        toks, gen, lps, plens = model.generate_continuous_with_logprobs(
+            prompts, max_new_tokens=48, temperature=1.0, top_k=None, eos_token_ids=EOS_IDS)
+        st = dict(model.last_stats)
+    finally:
+        model.decode_lookahead = True
+    early = _check_eos_retirement(gen, lps, 48)
+    assert early >= 3 and st["eos_finished"] >= early
+    assert st["blocks_in_use"] == 0
+    if lookahead:
+        assert st["lookahead_steps"] > 0 and st["discarded_rows"] > 0
+    else:
+        assert st["lookahead_steps"] == 0 and st["discarded_rows"] == 0
+    _assert_logprobs_match_oracle(model, toks, lps, plens, tag=f"EOS lookahead={lookahead}")
+
+
+def test_eos_lookahead_agrees_with_synchronous_engine(pkg, model):
+    """The lookahead engine with EOS retirement against the synchronous one.
+    A token's random number is keyed by (call seed, sequence, position), so
+    both draw the same tokens; the lookahead's extra (discarded) rows change
+    only how the attention splits the keys of a step, a rounding-level
+    difference, so sequences agree up to a draw that lands within rounding of
+    a cumulative-probability boundary."""
+    g = torch.Generator().manual_seed(41)
+    prompts = [torch.randint(0, VOCAB, (1, n), generator=g) for n in (40, 200, 90, 260, 12, 150)]
+    runs = []
+    for la in (False, True):
+        model.decode_lookahead = la
+        try:
+            torch.manual_seed(12)
+            print(f"[model] EOS sync vs lookahead: lookahead={la}", flush=True)
+            runs.append(model.generate_continuous_with_logprobs(
+                prompts, max_new_tokens=40, temperature=1.0, top_k=None, eos_token_ids=EOS_IDS))
+        finally:
+            model.decode_lookahead = True
+    (_, g0, l0, _), (_, g1, l1, _) = runs
+    same = agree = total = 0
+    for a, b, la_, lb_ in zip(g0, g1, l0, l1):
+        n = next((j for j, (x, y) in enumerate(zip(a, b)) if x != y), min(len(a), len(b)))
+        agree += n
+        total += max(len(a), len(b))
+        if a == b:
+            same += 1
+            assert max(abs(x - y) for x, y in zip(la_, lb_)) <= 0.07  # one bf16 ulp at |x| < 16
+    assert same >= len(prompts) - 1 and agree >= 0.9 * total, (same, agree, total)
+
+
+def test_topk_rollout_logprobs_match_oracle(pkg, model):
+    """The reference's default sampling (top_k = 20, temperature 0.6) through
+    the fused lm_head top-k sampler, against the oracle teacher-forced on the
+    engine's tokens: each token lies in the oracle's top 20 at its position,
+    and its log-probability under the top-20 distribution matches.  The 20th
+    and 21st logits are often within a bf16 ulp of each other, so where the
+    engine's token is the oracle's 21st (the rounding of the engine's own
+    hidden states ordered them the other way) the set with the two swapped is
+    the reference set."""
+    g = torch.Generator().manual_seed(42)
+    prompts = [torch.randint(0, VOCAB, (1, n), generator=g) for n in (33, 280, 100)]
+    k, temp = 20, 0.6
+    torch.manual_seed(13)
+    print("[model] top-k rollout vs oracle", flush=True)
+    toks, gen, lps, plens = model.generate_continuous_with_logprobs(
+        prompts, max_new_tokens=20, temperature=temp, top_k=k)
+    assert [len(x) for x in gen] == [20] * 3
+    diffs = {"bf16": [], "fp32": []}
+    swapped = 0
+    for b in range(len(toks)):
+        plen = plens[b]
+        for mode in diffs:
+            logits = OM.qwen3_logits(model.state_dict(), torch.as_tensor(toks[b][:-1])[None],
+                                     LAYERS, mode=mode)[0][plen - 1:].double() / temp
+            for j, t in enumerate(toks[b][plen:]):
+                x = logits[j]
+                order = np.lexsort((np.arange(VOCAB), -x.numpy())).tolist()
+                rank = order.index(t)
+                assert rank <= k, (b, j, rank)
+                kept = order[:k] if rank < k else order[:k - 1] + [t]
+                swapped += rank == k
+                ref = x[t] - torch.logsumexp(x[kept], 0)
+                diffs[mode].append(abs(lps[b][j] - ref.item()))
+    d16, d32 = torch.tensor(diffs["bf16"]), torch.tensor(diffs["fp32"])
+    print(f"[model] top-k log-prob |engine - oracle|: bf16 max {d16.max():.5f} mean "
+          f"{d16.mean():.6f}; fp32 max {d32.max():.5f} mean {d32.mean():.6f}; "
+          f"boundary swaps {swapped}", flush=True)
+    # the bars of the temperature-1 tests, scaled by 1 / T
+    assert d16.max() <= LP_BF16_MAX / temp and d16.mean() <= LP_BF16_MEAN / temp
+    assert d32.max() <= LP_FP32_MAX / temp and d32.mean() <= LP_FP32_MEAN / temp
+
+
+def test_graph_capture_failure_falls_back_to_eager(pkg, gpu, monkeypatch):
+    """If HIP graph capture fails (qwen3_naive.py:1126-1128) the engine decodes
+    eagerly: generation completes with the same tokens as an eager run."""
+    cfg = pkg.Qwen3Config(num_hidden_layers=1, vocab_size=VOCAB, tie_word_embeddings=False)
+    torch.manual_seed(0)
+    m = pkg.Qwen3ForCausalLM(cfg)
+    with torch.no_grad():
+        for name, p in m.named_parameters():
+            p.uniform_(0.8, 1.2) if "norm" in name else p.normal_(0, 0.05)
+    m = m.to(gpu).to(torch.bfloat16).eval()
+    m.allocate_global_kv_cache(num_blocks=8)
+    prompts = [torch.randint(0, VOCAB, (1, n), generator=torch.Generator().manual_seed(n))
+               for n in (10, 40)]
+
+    def refuse(*args, **kwargs):
+        raise RuntimeError("capture refused")
+    monkeypatch.setattr(torch.cuda, "graph", refuse)
+    print("[model] capture failure -> eager", flush=True)
+    torch.manual_seed(4)
+    _, gen_fb = m.generate_continuous(prompts, max_new_tokens=6, temperature=1.0, top_k=None)
+    assert not m._has_cuda_graphs and m.last_stats["graph_steps"] == 0
+    assert [len(x) for x in gen_fb] == [6, 6]
+    monkeypatch.undo()
+    torch.manual_seed(4)
+    _, gen_eager = m.generate_continuous(prompts, max_new_tokens=6, temperature=1.0, top_k=None,
+                                         use_graphs=False)
+    assert gen_fb == gen_eager
+
+
+def test_hidden_wider_than_norm_kernels(pkg, gpu):
+    """A model whose hidden size (5,120, as Qwen3-14B/32B) exceeds the RMSNorm
+    kernels' 4,096-wide rows: the norms run as torch ops and the decode
+    projections return dense outputs (no split-K partials), and the engine's
+    log-probabilities still match the oracle."""
+    cfg = pkg.Qwen3Config(hidden_size=5120, intermediate_size=1024, num_hidden_layers=1,
+                          vocab_size=VOCAB, tie_word_embeddings=False)
+    torch.manual_seed(1)
+    m = pkg.Qwen3ForCausalLM(cfg)
+    with torch.no_grad():
+        for name, p in m.named_parameters():
+            if "norm" in name:
+                p.uniform_(0.8, 1.2)
+            elif "embed" in name:
+                p.normal_(0, 0.25)
+            elif "lm_head" in name:
+                p.normal_(0, 0.05)
+            elif p.dim() == 2:
+                p.normal_(0, 0.01)
+    m = m.to(gpu).to(torch.bfloat16).eval()
+    m.allocate_global_kv_cache(num_blocks=8)
+    g = torch.Generator().manual_seed(50)
+    prompts = [torch.randint(0, VOCAB, (1, n), generator=g) for n in (17, 90)]
+    torch.manual_seed(6)
+    print("[model] hidden 5120", flush=True)
+    toks, gen, lps, plens = m.generate_continuous_with_logprobs(prompts, max_new_tokens=8,
+                                                                temperature=1.0, top_k=None)
+    assert [len(x) for x in gen] == [8, 8] and m.last_stats["graph_steps"] > 0
+    _assert_logprobs_match_oracle(m, toks, lps, plens, n_layers=1, tag="hidden 5120")

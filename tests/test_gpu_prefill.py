@@ -181,6 +181,72 @@ def test_prefill_graph_replay_matches_eager(pkg, gpu):
         assert torch.equal(out, eager)
 
 
+def _queue_case(gpu, n_seqs, seed):
+    """A launch on the persistent work queue (its counters live in the
+    workspace): n_seqs 512-token chunks after a 1,024-token prefix."""
+    lens_q = [512] * n_seqs
+    lens_k = [1024 + n for n in lens_q]
+    kc, vc, bt = _pool(seed, lens_k)
+    cu_q, cu_k = [0], [0]
+    for a, c in zip(lens_q, lens_k):
+        cu_q.append(cu_q[-1] + a)
+        cu_k.append(cu_k[-1] + c)
+    g = torch.Generator().manual_seed(seed + 1)
+    q = torch.randn(cu_q[-1], 16, 128, generator=g).to(torch.bfloat16)
+    args = (q.to(gpu), kc.to(gpu), vc.to(gpu), torch.tensor(cu_q, dtype=torch.int32, device=gpu),
+            torch.tensor(cu_k, dtype=torch.int32, device=gpu), 512, max(lens_k), SCALE, True,
+            bt.to(gpu))
+    return args, (q, kc, vc, cu_q, cu_k, bt)
+
+
+def test_prefill_graph_keeps_private_workspace(pkg, gpu):
+    """A captured prefill owns its workspace: an eager call that outgrows the
+    cached workspace (which frees it) before the replays changes nothing, and
+    every replay equals the eager result."""
+    small, ref_small = _queue_case(gpu, 10, 60)
+    big, _ = _queue_case(gpu, 20, 61)
+    print("[prefill] graph with private workspace", flush=True)
+    eager0 = pkg.kernels.varlen_prefill_attention(*small)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        pkg.kernels.varlen_prefill_attention(*small)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = pkg.kernels.varlen_prefill_attention(*small)
+    for it in range(3):
+        pkg.kernels.varlen_prefill_attention(*big)     # grows (replaces) the cached workspace
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager0), it
+        assert torch.equal(pkg.kernels.varlen_prefill_attention(*small), eager0)
+    _check(out, *ref_small)
+
+
+def test_prefill_two_streams_do_not_share_counters(pkg, gpu):
+    """Prefill calls on two streams at once (each stream its own cached
+    workspace, so the work-queue counters are never shared) give the results
+    of the calls made one after the other."""
+    a, _ = _queue_case(gpu, 10, 70)
+    b, _ = _queue_case(gpu, 12, 71)
+    want_a = pkg.kernels.varlen_prefill_attention(*a).clone()
+    want_b = pkg.kernels.varlen_prefill_attention(*b).clone()
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    print("[prefill] two streams", flush=True)
+    for it in range(3):
+        s1.wait_stream(torch.cuda.current_stream())
+        s2.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s1):
+            out_a = pkg.kernels.varlen_prefill_attention(*a)
+        with torch.cuda.stream(s2):
+            out_b = pkg.kernels.varlen_prefill_attention(*b)
+        torch.cuda.synchronize()
+        assert torch.equal(out_a, want_a) and torch.equal(out_b, want_b), it
+
+
 def test_prefill_rejects_bad_inputs(pkg, gpu):
     kc, vc, bt = _pool(18, [10])
     q = torch.zeros(10, 16, 128, dtype=torch.bfloat16, device=gpu)

@@ -61,6 +61,23 @@ def test_uniform53_layout_and_range():
     assert len(set(u.tolist())) == 5
 
 
+def test_uniform53_row_counters():
+    """Row counter q occupies counter words 1-2: q = r reproduces the default
+    layout, and q = (j << 32) | s is row s's block of a call at offset + j."""
+    seed, off = (7 << 32) | 3, (2 << 32) | 11
+    assert (OS.uniform53(6, seed, off, np.arange(6)) == OS.uniform53(6, seed, off)).all()
+    q = [(5 << 32) | 4, (0 << 32) | 1, (9 << 32) | 0]
+    got = OS.uniform53(3, seed, off, q)
+    assert got[0] == OS.uniform53(5, seed, off + 5)[4]
+    assert got[1] == OS.uniform53(2, seed, off)[1]
+    assert got[2] == OS.uniform53(1, seed, off + 9)[0]
+    # the low word of the offset wraps into nothing: (offset_lo + hi32(q)) mod 2^32
+    w = OS.philox4x32_10(np.array([[0, 4, (0xFFFFFFFF + 5) & 0xFFFFFFFF, 0]], dtype=np.uint32),
+                         (3, 7))[0]
+    want = (((int(w[0]) << 21) | (int(w[1]) >> 11)) + 0.5) / 2 ** 53
+    assert OS.uniform53(1, seed, 0xFFFFFFFF, [(5 << 32) | 4])[0] == want
+
+
 def test_inverse_cdf_closed_forms():
     # p = softmax([0, 0]) = (1/2, 1/2): u below 1/2 draws 0, above draws 1.
     x = torch.zeros(2, 2)
