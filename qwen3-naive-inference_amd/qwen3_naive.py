@@ -399,8 +399,10 @@ class Qwen3ForCausalLM(nn.Module):
         self._graph_bufs = None
         self._graph_pool = None
         self._has_cuda_graphs = False
-        # Launch decode step t+1 before reading step t's tokens back (EOS-free runs).
+        # Launch decode step t+1 before reading step t's tokens back.
         self.decode_lookahead = True
+        self._preemptions = 0
+        self._preempted: set = set()
 
     def forward(self, x):
         return self.lm_head(self.model(x))
@@ -627,6 +629,7 @@ class Qwen3ForCausalLM(nn.Module):
                         running.pop()
                         waiting.appendleft(victim)
                         self._preemptions += 1
+                        self._preempted.add(getattr(victim, "seq_index", -1))
                         if victim is seq:
                             break
                     if seq.status == "WAITING":
@@ -721,6 +724,7 @@ class Qwen3ForCausalLM(nn.Module):
         seed = int(torch.randint(0, 2 ** 62, (1,)).item())  # one per call (torch.manual_seed)
         running: list[Sequence] = []
         self._preemptions = 0
+        self._preempted = set()
         self.last_stats = {"steps": 0, "decode_steps": 0, "graph_steps": 0, "unit_graph_steps": 0,
                            "lookahead_steps": 0, "eos_finished": 0, "discarded_rows": 0}
         dev = self._device()
@@ -882,6 +886,7 @@ class Qwen3ForCausalLM(nn.Module):
                 s.num_scheduled_tokens = 0
         flush()
         self.last_stats["preemptions"] = self._preemptions
+        self.last_stats["preempted_seqs"] = sorted(self._preempted)
         self.last_stats["blocks_in_use"] = self._num_blocks - bm.available
         return all_seqs
 
