@@ -232,6 +232,57 @@ def leg_decode_step(torch, pkg, dev, steps, warmup, w, attn_ms_step):
     return out
 
 
+def leg_decode_step256(torch, pkg, dev, steps, warmup, ctx_len=640, bsz=256):
+    """The rollout's decode step: 256 sequences at the rollout's mean context
+    (640 cached keys; all sequences of a rollout step have near-equal contexts),
+    the 28-layer model with one K/V page pool slice per layer as the engine
+    allocates it, replayed through the engine's own decode path
+    (``_run_decode_graph_seqs``: one host-to-device copy of the step's inputs,
+    then the whole-unit graph of the 256-row bucket); then with the fused
+    lm_head + sampler (all entries, and the top 20)."""
+    log(f"decode_step256: {bsz} sequences x {ctx_len} keys, 28 layers")
+    model = make_qwen3(torch, pkg, dev)
+    pages = bsz * ((ctx_len + 1 + 255) // 256) + 2
+    model.allocate_global_kv_cache(num_blocks=pages)
+    for layer in model.model.layers:
+        layer.self_attn.k_cache.normal_()
+        layer.self_attn.v_cache.normal_()
+    model._ensure_engine(True, bt_width=(ctx_len + 1 + 255) // 256)
+    bm = pkg.BlockManager(pages)
+    g = torch.Generator().manual_seed(1)
+    seqs = []
+    for _ in range(bsz):
+        s = pkg.Sequence(torch.randint(0, 151936, (ctx_len + 1,), generator=g).tolist())
+        bm.allocate(s)
+        s.kv_len = ctx_len
+        s.num_scheduled_tokens = 1
+        seqs.append(s)
+    model.last_stats = {}
+    with torch.no_grad():
+        step = lambda: model._run_decode_graph_seqs(seqs)
+        body_ms, _ = timed_launches(torch, [step], steps, warmup)
+        body_ms /= steps
+        unit_graph = model.last_stats.get("unit_graph_steps", 0) > 0
+        h = step()
+        rec = {}
+        for name, k in (("sample", None), ("topk20", 20)):
+            ms, _ = timed_launches(torch, [lambda: (step(), model._sample(h, 1.0, k, True))],
+                                   steps, warmup)
+            rec[f"ms_per_step_with_lm_head_and_{name}"] = ms / steps
+    kv = 28 * bsz * (ctx_len + 1) * 8 * 128 * 2 * 2
+    weights = sum(p.numel() * 2 for p in model.parameters())
+    out = dict(ms_per_step=body_ms, us_per_layer=body_ms * 1e3 / 28, batch=bsz,
+               context=ctx_len, whole_unit_graph=unit_graph, kv_bytes_per_step=kv,
+               weight_bytes=weights, hbm_gbs=(kv + weights) / (body_ms * 1e-3) / 1e9, **rec)
+    model._graphs, model._graphs_units, model._graph_bufs, model._graph_pool = {}, {}, None, None
+    for layer in model.model.layers:
+        layer.self_attn.k_cache = layer.self_attn.v_cache = None
+    del model, h
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return out
+
+
 def W_kv_bytes(w) -> int:
     """K/V bytes a 28-layer decode step reads (ctx + 1 keys per sequence and layer)."""
     return int(w["k_cache"].shape[0]) * int(w["kv_bytes"])
@@ -1185,7 +1236,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--legs",
-                    default="decode1,decode,decode_step,lm_head,grpo,store,prefill,norm_rope,host,rollout")
+                    default="decode1,decode,decode_step,decode_step256,lm_head,grpo,store,prefill,norm_rope,host,"
+                            "rollout")
     ap.add_argument("--rollout-tokens", type=int, default=1024,
                     help="new tokens per sequence in the end-to-end rollout leg")
     ap.add_argument("--rollout-compare-tokens", type=int, default=64,
@@ -1238,6 +1290,9 @@ def main() -> int:
                                                      results["decode"]["ms_per_step"])
         del results["decode"]["workload"]
         torch.cuda.empty_cache()
+    if "decode_step256" in legs:
+        results["decode_step256"] = leg_decode_step256(torch, pkg, dev, max(5, args.steps // 2),
+                                                       args.warmup)
     if "lm_head" in legs:
         results["lm_head"] = leg_lm_head(torch, pkg, dev, args.steps, args.warmup)
     if "grpo" in legs:
@@ -1324,6 +1379,17 @@ def main() -> int:
             "attention_share": round(r["attention_share"], 4),
             "kv_bytes_per_step": r["kv_bytes_per_step"], "weight_bytes": r["weight_bytes"],
             "hbm_gbs_kv_plus_weights": round(r["hbm_gbs"], 1),
+            "frac_of_hbm_peak": round(r["hbm_gbs"] / HBM_PEAK_GBS, 4)}
+
+    if "decode_step256" in results:
+        r = results["decode_step256"]
+        secondary["decode_step_28layer_b256_rollout_shape"] = {
+            "workload": "the rollout's decode step: 256 sequences x 640 cached keys (its mean "
+                        "context), random-init Qwen3-0.6B bf16, 28 per-layer page pools, through "
+                        "the engine's decode path (one input copy, then the whole-unit HIP graph "
+                        "of the 256-row bucket); then the fused lm_head + sampler, all entries "
+                        "and top 20",
+            **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()},
             "frac_of_hbm_peak": round(r["hbm_gbs"] / HBM_PEAK_GBS, 4)}
 
     if "host" in results:
@@ -1437,7 +1503,7 @@ def main() -> int:
                 "traffic_note": "HBM bytes per launch (split + merge) from rocprofv3 FETCH_SIZE x2.0 "
                                 "+ WRITE_SIZE x1.0 passes of this leg, "
                                 "profiles/paged_decode_28layer_b64_ctx1024-4096.md",
-                "kernel": "decode_streamk_split<8,2> (+ decode_streamk_merge<8,2>)",
+                "kernel": "decode_streamk_split<8, 2, 8, false> (+ decode_streamk_merge<8, 2, 8>)",
                 "us_per_launch": round(d["avg_launch_us"], 2),
                 "bytes_per_launch": d["bytes_per_launch"]},
             "cpu_baseline": cpu,
