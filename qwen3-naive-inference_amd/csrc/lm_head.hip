@@ -65,6 +65,7 @@ constexpr int kKC = 64;             // hidden elements per staged chunk
 constexpr int kRowB = kKC * 2;      // bytes per staged row
 constexpr int kRowThreads = 256;    // kernel 2
 constexpr int kMaxFusedTopK = 64;   // largest k of the fused top-k sampler
+constexpr int kMaxCandTiles = 2048; // vocabulary tiles the top-k row kernel holds in LDS
 constexpr int kMaxHidden = 16384;
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
@@ -84,7 +85,11 @@ __device__ __forceinline__ uint32_t value_key16(float xr) {
   return (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
 }
 __device__ __forceinline__ uint32_t cand_key(float xr, int local) {
-  return (value_key16(xr) << 16) | (0xffffu ^ (uint32_t)local);
+  // The value key is the high half of bits ^ (sign ? ~0 : 0x80000000) (the
+  // low 16 bits of a bf16-rounded value are zero).
+  const uint32_t b = __float_as_uint(xr);
+  const uint32_t m = (uint32_t)((int32_t)b >> 31) | 0x80000000u;
+  return ((b ^ m) & 0xffff0000u) | (0xffffu ^ (uint32_t)local);
 }
 __device__ __forceinline__ float key_value(uint32_t key) {
   const uint32_t k = key >> 16;
@@ -290,6 +295,10 @@ __global__ __launch_bounds__(NW * 64) void lmhead_items(
     const int64_t vbase = v0 + VW * vq + 4 * g4;
     const int vt = (int)(v0 / kTV) + (VW * vq) / kTV;  // this wave's 128-row tile
     const int lbase = (VW * vq) % kTV + 4 * g4;        // its first entry within the tile
+    // Only an item that reaches past the end of the vocabulary checks each
+    // entry (a wave-uniform choice between two copies of the loop).
+    const int vrel = vocab - (int)vbase;  // entries of this lane's columns that exist: j < vrel
+    auto rows = [&](auto check) __attribute__((always_inline)) {
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
       const int row_l = 64 * rq + 16 * rb + l16;
@@ -314,7 +323,7 @@ __global__ __launch_bounds__(NW * 64) void lmhead_items(
         for (int vb = 0; vb < VB; ++vb)
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            if (vbase + 16 * vb + e < vocab) t.insert(cand_key(acc[vb][rb][e], lbase + 16 * vb + e));
+            if (!check || 16 * vb + e < vrel) t.insert(cand_key(acc[vb][rb][e], lbase + 16 * vb + e));
         t = top4_pair_union<16>(t);
         t = top4_pair_union<32>(t);
         if constexpr (WPT > 1) {
@@ -329,7 +338,7 @@ __global__ __launch_bounds__(NW * 64) void lmhead_items(
       for (int vb = 0; vb < VB; ++vb)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const bool ok = vbase + 16 * vb + e < vocab;
+          const bool ok = !check || 16 * vb + e < vrel;
           acc[vb][rb][e] = ok ? acc[vb][rb][e] * c2 : kNegBig;
           mx = fmaxf(mx, acc[vb][rb][e]);
         }
@@ -355,6 +364,11 @@ __global__ __launch_bounds__(NW * 64) void lmhead_items(
 #pragma unroll
       for (int vb = 0; vb < VB; ++vb) acc[vb][rb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
+    };
+    if (v0 + TV <= vocab)
+      rows(std::false_type{});
+    else
+      rows(std::true_type{});
     if constexpr (WPT > 1) {
       __syncthreads();
       for (int r = tid; r < MT; r += NW * 64) {
@@ -663,9 +677,11 @@ __global__ __launch_bounds__(kRowThreads) void lmhead_topk_rows(
   __shared__ float kept_x[kMaxFusedTopK];  // logit * c2
   __shared__ int pick_sm;
   __shared__ __align__(16) uint16_t hrow[kMaxHidden];
+  __shared__ uint4 cr[kMaxCandTiles];  // the row's candidates, read once
   const int tid = threadIdx.x;
   const int row = blockIdx.x;
-  const uint4* cr = cand + (int64_t)row * n_vtiles;
+  const uint4* crg = cand + (int64_t)row * n_vtiles;
+  for (int t = tid; t < n_vtiles; t += kRowThreads) cr[t] = crg[t];
   const int cpt = (n_vtiles + kRowThreads - 1) / kRowThreads;
   const int lo = min(n_vtiles, tid * cpt), hi = min(n_vtiles, lo + cpt);
   if (tid == 0) n_sat = 0;
@@ -987,6 +1003,7 @@ extern "C" int qmi_lm_head_sample(const uint16_t* hidden_states, int64_t h_strid
   if (top_k < 0 || top_k > kMaxFusedTopK) return QMI_E_UNSUPPORTED;
   if (n_rows == 0 && vocab > 0 && hidden > 0) return QMI_OK;
   const bool topk = top_k > 0 && top_k < vocab;  // k >= vocab keeps every entry
+  if (topk && n_vtiles_of(vocab) > kMaxCandTiles) return QMI_E_UNSUPPORTED;
   int st = check_args(hidden_states, h_stride, n_rows, weight, w_stride, vocab, hidden, workspace,
                       workspace_bytes, topk);
   if (st != QMI_OK) return st;

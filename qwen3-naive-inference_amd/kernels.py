@@ -704,7 +704,8 @@ def sample_tokens_topk(logits: torch.Tensor, top_k: int, temperature: float = 1.
     return tok, lp
 
 
-MAX_FUSED_TOP_K = 64  # largest k the fused lm_head top-k sampler takes
+MAX_FUSED_TOP_K = 64            # largest k the fused lm_head top-k sampler takes
+MAX_FUSED_TOP_K_VOCAB = 262144  # and the largest vocabulary it takes it over
 
 
 def _lm_head_args(hidden: torch.Tensor, weight: torch.Tensor, top_k: int = 0):
@@ -749,6 +750,8 @@ def lm_head_sample(hidden: torch.Tensor, weight: torch.Tensor, temperature: floa
     k = 0 if top_k is None else int(top_k)
     if not 0 <= k <= MAX_FUSED_TOP_K:
         raise ValueError(f"top_k must be None or in [1, {MAX_FUSED_TOP_K}], got {top_k}")
+    if 0 < k < weight.shape[0] and weight.shape[0] > MAX_FUSED_TOP_K_VOCAB:
+        raise ValueError(f"fused top-k takes vocabularies up to {MAX_FUSED_TOP_K_VOCAB}")
     hidden, n, v, hdim, ws = _lm_head_args(hidden, weight, k)
     if seed is None:
         seed = int(torch.randint(0, 2 ** 62, (1,)).item())

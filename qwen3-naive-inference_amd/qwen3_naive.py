@@ -679,7 +679,8 @@ class Qwen3ForCausalLM(nn.Module):
         if top_k is not None and top_k >= w.shape[0]:
             top_k = None  # keeping every entry is plain sampling
         kern = h.dtype == torch.bfloat16 and h.is_cuda and w.dtype == torch.bfloat16
-        if kern and (top_k is None or top_k <= K.MAX_FUSED_TOP_K):
+        if kern and (top_k is None or (top_k <= K.MAX_FUSED_TOP_K
+                                       and w.shape[0] <= K.MAX_FUSED_TOP_K_VOCAB)):
             return K.lm_head_sample(h, w, temperature, seed=seed, want_logprobs=want_logprobs,
                                     top_k=top_k, row_counters=row_counters)
         if kern and top_k <= 1024:
