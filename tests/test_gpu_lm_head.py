@@ -94,6 +94,24 @@ def test_lm_head_logprob_matches_oracle(pkg, gpu, n, vocab, w_std):
         assert _rel(lp_exact, lp.cpu().double()) > 2 * LP_TOL
 
 
+def test_lm_head_logprob_many_row_tiles(pkg, gpu):
+    """Loss-step shapes (several 256-row tiles, items ordered per XCD): rows of
+    a 1,100-row call match the oracle and equal, bit for bit, the same rows
+    computed in a 300-row call."""
+    h, w, hg, wg = _inputs(gpu, 1100, 151936, w_std=0.05, seed=17)
+    tgt = torch.randint(0, 151936, (1100,), generator=torch.Generator().manual_seed(18))
+    print("[lm_head] logprob 1100 rows", flush=True)
+    lp, lse = pkg.kernels.lm_head_logprob(hg, wg, tgt.to(gpu))
+    lp3, lse3 = pkg.kernels.lm_head_logprob(hg[:300], wg, tgt[:300].to(gpu))
+    torch.cuda.synchronize()
+    assert torch.equal(lp[:300], lp3) and torch.equal(lse[:300], lse3)
+    rows = torch.tensor([0, 1, 255, 256, 511, 700, 1023, 1024, 1099])
+    xr, lo, hi = _logits_bf16(h[rows], w)
+    ref_lse = torch.logsumexp(xr, -1)
+    assert _lp_err(lp.cpu()[rows], xr, lo, hi, tgt[rows], ref_lse).max().item() <= LP_TOL
+    assert _rel(lse.cpu()[rows], ref_lse) <= LP_TOL
+
+
 def test_lm_head_logprob_equals_unfused_bf16_path(pkg, gpu):
     """The fused log-prob equals log_softmax over the bf16 logits of a torch
     GEMM (the autograd path: lm_head, then the log-softmax gather kernel) up to
