@@ -39,7 +39,7 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 # measured by two rocprofv3 --pmc passes (FETCH_SIZE scaled by 2.0, WRITE_SIZE by
 # 1.0, the factors a plain copy of known size gives); recorded in
 # profiles/paged_decode_28layer_b64_ctx1024-4096.md.
-DECODE_TRAFFIC_BYTES = 672384785
+DECODE_TRAFFIC_BYTES = 671878759
 METRIC = "decode-attn HBM GB/s (% of 8 TB/s); GRPO rollout tokens/s on 1 GPU"
 
 
