@@ -577,3 +577,30 @@ def test_hidden_wider_than_norm_kernels(pkg, gpu):
                                                                 temperature=1.0, top_k=None)
     assert [len(x) for x in gen] == [8, 8] and m.last_stats["graph_steps"] > 0
     _assert_logprobs_match_oracle(m, toks, lps, plens, n_layers=1, tag="hidden 5120")
+
+
+@pytest.mark.parametrize("lookahead", [False, True])
+def test_eos_rollout_under_preemption(pkg, model, lookahead):
+    """EOS retirement and LIFO preemption together: four ~250-token prompts
+    in a 6-page pool (8 pages would be needed), EOS ids drawn now and then.
+    Every sequence ends at its first EOS or after the token budget, every
+    page is released, and the log-probs (victims' included) match the
+    oracle."""
+    g = torch.Generator().manual_seed(43)
+    prompts = [torch.randint(0, VOCAB, (1, n), generator=g) for n in (250, 240, 251, 245)]
+    model.allocate_global_kv_cache(num_blocks=6)
+    model.decode_lookahead = lookahead
+    try:
+        torch.manual_seed(14)
+        print(f"[model] EOS + preemption lookahead={lookahead}", flush=True)
+        toks, gen, lps, plens = model.generate_continuous_with_logprobs(
+            prompts, max_new_tokens=40, temperature=1.0, top_k=None, eos_token_ids=EOS_IDS)
+        st = dict(model.last_stats)
+    finally:
+        model.decode_lookahead = True
+        model._num_blocks = 0
+        model.allocate_global_kv_cache(num_blocks=64)
+    _check_eos_retirement(gen, lps, 40)
+    assert st["blocks_in_use"] == 0 and st["eos_finished"] >= 1
+    assert st["preemptions"] > 0 or st["eos_finished"] >= 3
+    _assert_logprobs_match_oracle(model, toks, lps, plens, tag=f"EOS+preemption la={lookahead}")
