@@ -981,14 +981,15 @@ def _timed(torch, fn):
 
 
 def leg_rollout(torch, pkg, dev, new_tokens=1024, compare_tokens=64, preempt_blocks=1200,
-                engines=("ours", "kernels", "torch"), runs_n=3, cpu=False):
+                engines=("ours", "kernels", "torch"), runs_n=3, cpu=False, eos_runs=True):
     """Config 5: 32 prompts x group 8 = 256 sequences, 128-token prompts, T=1.0,
     no top-k, ``new_tokens`` generated tokens each, continuous batching with the
     2048-token step budget and LIFO preemption, ~40 GB pool (1,362 blocks: no
     preemption); then the GRPO loss over the generated tokens.  Also: the same
     rollout in a ``preempt_blocks`` pool (under the 1,280 blocks 256 x 5 pages
     need, so LIFO preemption fires), and ours against the reference engine's
-    loop (ReferenceEngine, two model bodies) at ``compare_tokens`` new tokens."""
+    loop (ReferenceEngine, two model bodies) at ``compare_tokens`` new tokens, and
+    (``eos_runs``) EOS-terminated rollouts in the ~40 GB pool."""
     model = make_rollout_model(torch, pkg, dev)
     prompts = rollout_prompts(torch)
     n_tok = len(prompts)
@@ -1057,6 +1058,25 @@ def leg_rollout(torch, pkg, dev, new_tokens=1024, compare_tokens=64, preempt_blo
                               **dict(model.last_stats))
         log(f"rollout: preemption run {gen_n / dt:.0f} tok/s, "
             f"{model.last_stats['preemptions']} preemptions")
+        model.allocate_global_kv_cache(num_blocks=out["num_blocks"])
+        model.generate_continuous_with_logprobs(prompts[:16], max_new_tokens=4, temperature=1.0,
+                                                top_k=None)
+    if eos_runs:
+        # EOS-terminated rollouts: Qwen3's end ids (<|endoftext|>, <|im_end|>), and a
+        # dense set (every 1,024th id: ~1e-3 per token on the random-init model, so
+        # about 60% of the sequences stop early and the decode batch thins out).
+        vocab = model.config.vocab_size
+        for name, ids in (("eos", [151643, 151645]), ("eos_varlen", list(range(7, vocab, 1024)))):
+            ids = [i for i in ids if i < vocab]
+            torch.manual_seed(2)
+            (_, gen_e, _, _), dt = _timed(torch, lambda: gen(new_tokens, eos_token_ids=ids))
+            gen_n = sum(len(x) for x in gen_e)
+            out[name] = dict(eos_ids=len(ids), generated=gen_n, rollout_s=dt,
+                             tokens_per_s=gen_n / dt,
+                             finished_early=sum(len(x) < new_tokens for x in gen_e),
+                             mean_new_tokens=gen_n / len(gen_e), **dict(model.last_stats))
+            log(f"rollout: {name} run {gen_n / dt:.0f} tok/s, "
+                f"{out[name]['finished_early']} sequences ended at EOS")
     if cpu:
         log("cpu baseline (oracle decode steps at batch 256)")
         out["cpu_baseline"] = cpu_baseline_rollout(torch, model)
@@ -1249,6 +1269,8 @@ def main() -> int:
                     help="pool of the forced-preemption rollout (0 skips it)")
     ap.add_argument("--rollout-runs", type=int, default=3,
                     help="timed full rollouts (median reported)")
+    ap.add_argument("--rollout-no-eos", action="store_true",
+                    help="skip the EOS-terminated rollout runs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 1 GiB device copy (counter calibration)")
@@ -1311,7 +1333,8 @@ def main() -> int:
                                          compare_tokens=args.rollout_compare_tokens,
                                          preempt_blocks=args.rollout_preempt_blocks,
                                          engines=tuple(args.rollout_engines.split(",")),
-                                         runs_n=args.rollout_runs, cpu=not args.no_cpu)
+                                         runs_n=args.rollout_runs, cpu=not args.no_cpu,
+                                         eos_runs=not args.rollout_no_eos)
 
     cpu_grpo = None
     if not args.no_cpu and "grpo" in results:
@@ -1446,6 +1469,18 @@ def main() -> int:
                 "rollout_s": round(pr["rollout_s"], 3), "preemptions": pr["preemptions"],
                 "engine_steps": pr["steps"], "graph_decode_steps": pr["graph_steps"],
                 "lookahead_decode_steps": pr["lookahead_steps"]}
+        for name, desc in (("eos", "Qwen3's end ids 151643 / 151645"),
+                           ("eos_varlen", "every 1,024th vocabulary id (lengths vary)")):
+            if name in r:
+                e = r[name]
+                secondary["grpo_rollout"][f"{name}_terminated"] = {
+                    "eos_token_ids": desc, "tokens_per_s": round(e["tokens_per_s"], 1),
+                    "generated_tokens": e["generated"], "rollout_s": round(e["rollout_s"], 3),
+                    "finished_early": e["finished_early"],
+                    "mean_new_tokens": round(e["mean_new_tokens"], 1),
+                    "engine_steps": e["steps"], "graph_decode_steps": e["graph_steps"],
+                    "lookahead_decode_steps": e["lookahead_steps"],
+                    "discarded_rows": e.get("discarded_rows")}
         if "ours_short" in r:
             o = r["ours_short"]
             cmp = {"new_tokens": args.rollout_compare_tokens,
