@@ -564,15 +564,37 @@ __device__ void tile_logits(const uint16_t* hrow, const uint16_t* __restrict__ w
   const uint16_t* wr0 = w + (vw + l16 < vocab ? vw + l16 : (int64_t)vocab - 1) * w_stride + 8 * g4;
   const uint16_t* wr1 = w + (vw + 16 + l16 < vocab ? vw + 16 + l16 : (int64_t)vocab - 1) * w_stride + 8 * g4;
   f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-  for (int k = 0; k < hidden; k += 64) {  // hidden is a multiple of 64
-    const uint4 a00 = load_u4(wr0 + k), a10 = load_u4(wr1 + k);
-    const uint4 a01 = load_u4(wr0 + k + 32), a11 = load_u4(wr1 + k + 32);
-    const bf16x8_t b0 = as_bf16x8(*reinterpret_cast<const uint4*>(hrow + k + 8 * g4));
-    const bf16x8_t b1 = as_bf16x8(*reinterpret_cast<const uint4*>(hrow + k + 32 + 8 * g4));
-    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a00), b0, acc0, 0, 0, 0);
-    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a10), b0, acc1, 0, 0, 0);
-    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a01), b1, acc0, 0, 0, 0);
-    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a11), b1, acc1, 0, 0, 0);
+  // The W pieces of 64-element steps go out kAhead steps before their MFMAs
+  // (a register ring), so the 2 KB-strided rows cost a few memory round trips
+  // rather than one per step.
+  constexpr int kAhead = 8;
+  const int n_it = hidden / 64;  // hidden is a multiple of 64
+  uint4 ring[kAhead][4];
+  auto fetch = [&](uint4* r, int it) __attribute__((always_inline)) {
+    const int k = 64 * it;
+    r[0] = load_u4(wr0 + k);
+    r[1] = load_u4(wr1 + k);
+    r[2] = load_u4(wr0 + k + 32);
+    r[3] = load_u4(wr1 + k + 32);
+  };
+#pragma unroll
+  for (int j = 0; j < kAhead; ++j)
+    if (j < n_it) fetch(ring[j], j);
+  for (int i0 = 0; i0 < n_it; i0 += kAhead) {
+#pragma unroll
+    for (int j = 0; j < kAhead; ++j) {
+      const int it = i0 + j;
+      if (it < n_it) {
+        const int k = 64 * it;
+        const bf16x8_t b0 = as_bf16x8(*reinterpret_cast<const uint4*>(hrow + k + 8 * g4));
+        const bf16x8_t b1 = as_bf16x8(*reinterpret_cast<const uint4*>(hrow + k + 32 + 8 * g4));
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ring[j][0]), b0, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ring[j][1]), b0, acc1, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ring[j][2]), b1, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ring[j][3]), b1, acc1, 0, 0, 0);
+        if (it + kAhead < n_it) fetch(ring[j], it + kAhead);
+      }
+    }
   }
   if (l16 == 0) {
 #pragma unroll
@@ -748,6 +770,26 @@ __global__ __launch_bounds__(kRowThreads) void lmhead_topk_rows(
       }
     }
   };
+  // The bin of the histogram that holds the need-th largest entry, by one
+  // block-wide scan (thread t takes bin 255 - t): the bin b with fewer than
+  // `need` entries above it and at least `need` from it up.  Returns b and
+  // the entries above it; with fewer than `need` entries in all, -1 (or, when
+  // `floor0`, bin 0 with everything above it).
+  auto find_bin = [&](int need, bool floor0, int* above_out) {
+    const int b = 255 - tid;
+    const int c = (int)hist[b];
+    int tot;
+    const int above = block_excl_scan_i32(c, smi, &tot);  // entries in bins > b
+    const bool hit = tot >= need ? (above < need && above + c >= need) : (floor0 && b == 0);
+    if (tot < need && !floor0 && tid == 0) sel[0] = -1;
+    if (hit) {
+      sel[0] = b;
+      sel[1] = above;
+    }
+    __syncthreads();
+    *above_out = sel[1];
+    return sel[0];
+  };
   // Radix select of the k-th largest value key (16 bits, high byte then low
   // byte); sel = {threshold, entries above it, entries equal to it that are
   // kept}.  Fewer than k entries in all: threshold 0, every entry kept.
@@ -756,19 +798,10 @@ __global__ __launch_bounds__(kRowThreads) void lmhead_topk_rows(
     __syncthreads();
     for_each([&](uint32_t key, int) { atomicAdd(&hist[key >> 24], 1u); });
     __syncthreads();
-    if (tid == 0) {
-      int cum = 0, b = 255;
-      for (; b >= 0; --b) {
-        if (cum + (int)hist[b] >= k) break;
-        cum += (int)hist[b];
-      }
-      sel[0] = b;     // high byte, or -1 when everything is kept
-      sel[1] = cum;
-    }
+    int cum;
+    const int hb = find_bin(k, false, &cum);  // high byte, or -1 when everything is kept
     __syncthreads();
-    const int hb = sel[0];
     if (hb < 0) {
-      __syncthreads();
       if (tid == 0) {
         sel[0] = 0;
         sel[2] = 0;
@@ -782,15 +815,13 @@ __global__ __launch_bounds__(kRowThreads) void lmhead_topk_rows(
       if ((int)(key >> 24) == hb) atomicAdd(&hist[(key >> 16) & 0xffu], 1u);
     });
     __syncthreads();
+    int above;
+    const int lb = find_bin(k - cum, true, &above);
+    __syncthreads();
     if (tid == 0) {
-      int cum = sel[1], b = 255;
-      for (; b > 0; --b) {
-        if (cum + (int)hist[b] >= k) break;
-        cum += (int)hist[b];
-      }
-      sel[0] = (hb << 8) | b;
-      sel[1] = cum;
-      sel[2] = k - cum;
+      sel[0] = (hb << 8) | lb;
+      sel[1] = cum + above;
+      sel[2] = k - (cum + above);
     }
     __syncthreads();
   };
