@@ -556,7 +556,7 @@ __device__ __forceinline__ void load_hrow(const uint16_t* __restrict__ hr, int h
 // the same order: 32 at a time, lane group g4 supplying elements 8 g4 .. +8
 // of each 32), every column of the B operand holding the row, so the values
 // are bit-identical to the ones lmhead_items reduced.
-__device__ void tile_logits(const uint16_t* hrow, const uint16_t* __restrict__ w,
+__device__ __forceinline__ void tile_logits(const uint16_t* hrow, const uint16_t* __restrict__ w,
                             int64_t w_stride, int vocab, int hidden, int tile, float* xs) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, g4 = lane >> 4;
@@ -566,36 +566,41 @@ __device__ void tile_logits(const uint16_t* hrow, const uint16_t* __restrict__ w
   f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
   // The W pieces of 64-element steps go out kAhead steps before their MFMAs
   // (a register ring), so the 2 KB-strided rows cost a few memory round trips
-  // rather than one per step.
+  // rather than one per step.  The steady-state loop has no conditional
+  // loads (a fetch past the last step re-reads the last step, unused), so
+  // the compiler's waits keep the ring in flight.
   constexpr int kAhead = 8;
   const int n_it = hidden / 64;  // hidden is a multiple of 64
   uint4 ring[kAhead][4];
   auto fetch = [&](uint4* r, int it) __attribute__((always_inline)) {
-    const int k = 64 * it;
+    const int k = 64 * min(it, n_it - 1);
     r[0] = load_u4(wr0 + k);
     r[1] = load_u4(wr1 + k);
     r[2] = load_u4(wr0 + k + 32);
     r[3] = load_u4(wr1 + k + 32);
   };
+  auto step = [&](const uint4* r, int it) __attribute__((always_inline)) {
+    const int k = 64 * it;
+    const bf16x8_t b0 = as_bf16x8(*reinterpret_cast<const uint4*>(hrow + k + 8 * g4));
+    const bf16x8_t b1 = as_bf16x8(*reinterpret_cast<const uint4*>(hrow + k + 32 + 8 * g4));
+    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(r[0]), b0, acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(r[1]), b0, acc1, 0, 0, 0);
+    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(r[2]), b1, acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(r[3]), b1, acc1, 0, 0, 0);
+  };
 #pragma unroll
-  for (int j = 0; j < kAhead; ++j)
-    if (j < n_it) fetch(ring[j], j);
-  for (int i0 = 0; i0 < n_it; i0 += kAhead) {
+  for (int j = 0; j < kAhead; ++j) fetch(ring[j], j);
+  int i0 = 0;
+  for (; i0 + kAhead <= n_it; i0 += kAhead) {
 #pragma unroll
     for (int j = 0; j < kAhead; ++j) {
-      const int it = i0 + j;
-      if (it < n_it) {
-        const int k = 64 * it;
-        const bf16x8_t b0 = as_bf16x8(*reinterpret_cast<const uint4*>(hrow + k + 8 * g4));
-        const bf16x8_t b1 = as_bf16x8(*reinterpret_cast<const uint4*>(hrow + k + 32 + 8 * g4));
-        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ring[j][0]), b0, acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ring[j][1]), b0, acc1, 0, 0, 0);
-        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ring[j][2]), b1, acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ring[j][3]), b1, acc1, 0, 0, 0);
-        if (it + kAhead < n_it) fetch(ring[j], it + kAhead);
-      }
+      step(ring[j], i0 + j);
+      fetch(ring[j], i0 + j + kAhead);
     }
   }
+#pragma unroll
+  for (int j = 0; j < kAhead; ++j)
+    if (i0 + j < n_it) step(ring[j], i0 + j);
   if (l16 == 0) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -620,12 +625,35 @@ __global__ __launch_bounds__(kRowThreads) void lmhead_sample_rows(
   const int tid = threadIdx.x;
   const int row = blockIdx.x;
   const float2* pr = part + (int64_t)row * n_vtiles;
-  load_hrow(h + (int64_t)row * h_stride, hidden, hrow);
   const int cpt = (n_vtiles + kRowThreads - 1) / kRowThreads;
-  double own, excl;
-  const RowLse L = row_lse(pr, n_vtiles, cpt, &own, &excl, smf, smd);
-
+  const int lo = min(n_vtiles, tid * cpt), hi = min(n_vtiles, lo + cpt);
+  // A thread's pairs are read once into registers when they fit (up to
+  // 2,048 tiles), in flight together with the hidden-state row; entries past
+  // its chunk hold (-big, 0), which add exactly zero to the fp64 sums.
+  constexpr int kPR = 8;
+  const bool regs = cpt <= kPR;
+  float2 pv[kPR];
+  if (regs) {
+#pragma unroll
+    for (int i = 0; i < kPR; ++i) pv[i] = lo + i < hi ? pr[lo + i] : make_float2(kNegBig, 0.f);
+  }
   const double u = row_uniform(row, row_ctr, seed_lo, seed_hi, off_lo, off_hi);
+  load_hrow(h + (int64_t)row * h_stride, hidden, hrow);
+  double own, excl;
+  RowLse L;
+  if (regs) {
+    float mx = kNegBig;
+#pragma unroll
+    for (int i = 0; i < kPR; ++i) mx = fmaxf(mx, pv[i].x);
+    L.m2 = block_max256(mx, smf);
+    double acc = 0.0;
+#pragma unroll
+    for (int i = 0; i < kPR; ++i) acc += (double)(pv[i].y * fast_exp2(pv[i].x - L.m2));
+    own = acc;
+    excl = block_excl_scan256(acc, smd, &L.s);
+  } else {
+    L = row_lse(pr, n_vtiles, cpt, &own, &excl, smf, smd);
+  }
   const double target = u * L.s;
 
   if (tid == 0) {
@@ -633,14 +661,29 @@ __global__ __launch_bounds__(kRowThreads) void lmhead_sample_rows(
     sel_resid = 0.0;
   }
   __syncthreads();
-  const int lo = min(n_vtiles, tid * cpt), hi = min(n_vtiles, lo + cpt);
   if (own > 0.0 && target >= excl && target < excl + own) {
     double cum = excl;
     int t = lo;
-    for (; t < hi - 1; ++t) {
-      const double p = (double)(pr[t].y * fast_exp2(pr[t].x - L.m2));
-      if (target < cum + p) break;
-      cum += p;
+    if (regs) {
+      bool found = false;
+#pragma unroll
+      for (int i = 0; i < kPR - 1; ++i) {
+        if (!found && lo + i < hi - 1) {
+          const double p = (double)(pv[i].y * fast_exp2(pv[i].x - L.m2));
+          if (target < cum + p) {
+            found = true;
+          } else {
+            cum += p;
+            t = lo + i + 1;
+          }
+        }
+      }
+    } else {
+      for (; t < hi - 1; ++t) {
+        const double p = (double)(pr[t].y * fast_exp2(pr[t].x - L.m2));
+        if (target < cum + p) break;
+        cum += p;
+      }
     }
     sel_tile = t;
     sel_resid = target - cum;
