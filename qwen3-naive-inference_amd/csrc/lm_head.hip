@@ -310,13 +310,16 @@ __global__ __launch_bounds__(NW * 64) void lmhead_items(
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) acc[vb][rb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  int64_t tgt_id[4] = {-1, -1, -1, -1};
+  // Target vocabulary index of each row block's row for this lane, -1 when
+  // out of range (such a row's log-prob is NaN, set by the row kernel).
+  int tgt_id[4] = {-1, -1, -1, -1};
   auto load_targets = [&](Pos it) __attribute__((always_inline)) {
     const int r0 = it.rt * MT;
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
       const int row = r0 + 64 * rq + 16 * rb + l16;
-      tgt_id[rb] = tgt[(int64_t)(row < n_rows ? row : n_rows - 1) * tgt_stride];
+      const int64_t t = tgt[(int64_t)(row < n_rows ? row : n_rows - 1) * tgt_stride];
+      tgt_id[rb] = t >= 0 && t < vocab ? (int)t : -1;
     }
   };
 
@@ -342,14 +345,18 @@ __global__ __launch_bounds__(NW * 64) void lmhead_items(
       for (int vb = 0; vb < VB; ++vb)
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc[vb][rb][e] = bf16_round(acc[vb][rb][e]);
-      if (tgt && row < n_rows) {  // the target's logit, by the lane holding it
-        const int64_t tl = tgt_id[rb] - vbase;  // 16 vb + e if this lane holds it
-        if (tl >= 0 && tl < VW && (tl & 12) == 0) {
+      if (tgt) {  // the target's logit, by the lane holding it
+        const int tl = tgt_id[rb] - (int)vbase;  // 16 vb + e if this lane holds it
+        const bool mine = row < n_rows && tgt_id[rb] >= 0 && tl >= 0 && tl < VW && (tl & 12) == 0;
+        // Few waves hold a target in a given row block (16 rows x VW entries of
+        // the vocabulary): the selection runs only in those, by conditional moves.
+        if (__ballot(mine) != 0ull) {
+          float v = 0.f;
 #pragma unroll
           for (int vb = 0; vb < VB; ++vb)
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (tl == 16 * vb + e) tgt_logit[row] = acc[vb][rb][e];
+            for (int e = 0; e < 4; ++e) v = tl == 16 * vb + e ? acc[vb][rb][e] : v;
+          if (mine) tgt_logit[row] = v;
         }
       }
       if constexpr (TOPK) {
