@@ -30,7 +30,9 @@
 //     16-byte piece c of staged row r sits at c ^ ((r / 2) % 8): the 16 rows
 //     a 16-lane group reads then cover all 64 LDS banks.
 //   * Up to 64 rows: items of 128 x 64, 4 waves of 32 vocabulary rows, three
-//     stages, two workgroups per CU.  Above: items of 256 x 256, 8 waves of
+//     stages, two workgroups per CU.  Up to 256 rows: items of 256 x 128, 8
+//     waves of 64 x 64 (two per 128-row tile), three stages, one workgroup per
+//     CU.  Above: items of 256 x 256, 8 waves of
 //     128 x 64 (one wave per 128-row vocabulary tile), two 64 KB stages, one
 //     workgroup per CU: each item re-reads its hidden-state rows from L2, so
 //     256-entry items halve that traffic per FLOP (at 8,192 rows 4.07 ->
@@ -413,21 +415,29 @@ __global__ __launch_bounds__(NW * 64) void lmhead_items(
       rows(std::true_type{});
     if constexpr (WPT > 1) {
       __syncthreads();
+      // Waves WPT tj .. WPT tj + WPT - 1 hold the item's tile tj.
       for (int r = tid; r < MT; r += NW * 64) {
         if (r0 + r < n_rows) {
-          float2 a = red[0][r];
 #pragma unroll
-          for (int j = 1; j < NVQ; ++j) lse2_merge(a.x, a.y, red[j][r].x, red[j][r].y);
-          part[(r0 + r) * (int64_t)n_vtiles + (int)(v0 / kTV)] = a;
-          if constexpr (TOPK) {
-            const uint4 k0 = redk[0][r];
-            Top4 t{k0.x, k0.y, k0.z, k0.w};
+          for (int tj = 0; tj < TVB; ++tj) {
+            const int vt = (int)(v0 / kTV) + tj;
+            if (vt < n_vtiles) {
+              float2 a = red[WPT * tj][r];
 #pragma unroll
-            for (int j = 1; j < NVQ; ++j) {
-              const uint4 kj = redk[j][r];
-              t.merge(Top4{kj.x, kj.y, kj.z, kj.w});
+              for (int j = 1; j < WPT; ++j)
+                lse2_merge(a.x, a.y, red[WPT * tj + j][r].x, red[WPT * tj + j][r].y);
+              part[(r0 + r) * (int64_t)n_vtiles + vt] = a;
+              if constexpr (TOPK) {
+                const uint4 k0 = redk[WPT * tj][r];
+                Top4 t{k0.x, k0.y, k0.z, k0.w};
+#pragma unroll
+                for (int j = 1; j < WPT; ++j) {
+                  const uint4 kj = redk[WPT * tj + j][r];
+                  t.merge(Top4{kj.x, kj.y, kj.z, kj.w});
+                }
+                cand[(r0 + r) * (int64_t)n_vtiles + vt] = make_uint4(t.c0, t.c1, t.c2, t.c3);
+              }
             }
-            cand[(r0 + r) * (int64_t)n_vtiles + (int)(v0 / kTV)] = make_uint4(t.c0, t.c1, t.c2, t.c3);
           }
         }
       }
@@ -1076,9 +1086,12 @@ int launch_tiles(const uint16_t* h, int64_t h_stride, int64_t n_rows, const uint
                  int64_t tgt_stride, bool topk, const LmWs& ws, hipStream_t s) {
   const int nvt = (int)n_vtiles_of(vocab);
   // Up to 64 rows: items of 128 x 64, 4 waves, three LDS stages, two 74 KB
-  // workgroups per CU.  Above: items of 256 x 256, 8 waves, two LDS stages,
-  // one 128 KB workgroup per CU.  A persistent grid of that many workgroups
-  // per CU, or fewer when there are fewer items.
+  // workgroups per CU.  Up to 256 rows: items of 256 x 128 (two row tiles at
+  // 256 rows, so 1,188 items for Qwen3's vocabulary instead of 594 -- 4 or 5
+  // per CU, not 2 or 3), 8 waves, three 48 KB stages, one workgroup per CU.
+  // Above: items of 256 x 256, 8 waves, two 64 KB stages, one workgroup per
+  // CU.  A persistent grid of that many workgroups per CU, or fewer when
+  // there are fewer items.
 #define QMI_LMI(MT, NW, NS, TVB, PER_CU, TOPK)                                                     \
   do {                                                                                            \
     const int nrt = (int)((n_rows + MT - 1) / MT);                                                \
@@ -1100,6 +1113,11 @@ int launch_tiles(const uint16_t* h, int64_t h_stride, int64_t n_rows, const uint
       QMI_LMI(64, 4, 3, 1, 2, true);
     else
       QMI_LMI(64, 4, 3, 1, 2, false);
+  } else if (n_rows <= 256) {
+    if (topk)
+      QMI_LMI(128, 8, 3, 2, 1, true);
+    else
+      QMI_LMI(128, 8, 3, 2, 1, false);
   } else {
     if (topk)
       QMI_LMI(256, 8, 2, 2, 1, true);
