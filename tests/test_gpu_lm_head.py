@@ -73,7 +73,7 @@ def _lp_err(lp, xr, lo, hi, tok, lse):
 
 
 @pytest.mark.parametrize("n,vocab,w_std", [(1, 2085, 0.05), (37, 2085, 0.2), (64, 151936, 0.05),
-                                           (100, 4096, 0.05), (300, 3000, 0.1)])
+                                           (100, 4096, 0.05), (130, 2085, 0.2), (300, 3000, 0.1)])
 def test_lm_head_logprob_matches_oracle(pkg, gpu, n, vocab, w_std):
     h, w, hg, wg = _inputs(gpu, n, vocab, w_std=w_std, seed=n)
     g = torch.Generator().manual_seed(n + 1)
@@ -143,7 +143,7 @@ def test_lm_head_logprob_out_of_range_target_is_nan(pkg, gpu):
 
 
 @pytest.mark.parametrize("n,vocab,temp", [(1, 2085, 1.0), (64, 151936, 1.0), (64, 151936, 0.6),
-                                          (256, 151936, 1.0), (300, 5000, 0.8)])
+                                          (130, 2085, 1.0), (256, 151936, 1.0), (300, 5000, 0.8)])
 def test_lm_head_sample_matches_oracle(pkg, gpu, n, vocab, temp):
     h, w, hg, wg = _inputs(gpu, n, vocab, w_std=0.1, seed=7 * n + vocab)
     seed, offset = 1234 + n, 99
