@@ -377,20 +377,26 @@ __global__ __launch_bounds__(NW * 64) void lmhead_items(
             cand[row * (int64_t)n_vtiles + vt] = make_uint4(t.c0, t.c1, t.c2, t.c3);
         }
       }
+      // (max, sum of exp2) of x c2 (c2 > 0, so the maximum is taken on the
+      // logits and scaled once); entries past the vocabulary add nothing.
       float mx = kNegBig;
 #pragma unroll
       for (int vb = 0; vb < VB; ++vb)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const bool ok = !check || 16 * vb + e < vrel;
-          acc[vb][rb][e] = ok ? acc[vb][rb][e] * c2 : kNegBig;
-          mx = fmaxf(mx, acc[vb][rb][e]);
+          mx = fmaxf(mx, ok ? acc[vb][rb][e] : kNegBig);
         }
+      mx *= c2;
       float sm = 0.f;
 #pragma unroll
       for (int vb = 0; vb < VB; ++vb)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sm += fast_exp2(acc[vb][rb][e] - mx);
+        for (int e = 0; e < 4; ++e) {
+          const bool ok = !check || 16 * vb + e < vrel;
+          const float p = fast_exp2(fmaf(acc[vb][rb][e], c2, -mx));
+          sm += ok ? p : 0.f;
+        }
       LanePair pm = lane_pair16(mx), ps = lane_pair16(sm);
       mx = pm.lo;
       sm = ps.lo;
