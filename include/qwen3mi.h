@@ -510,7 +510,8 @@ int qmi_sample_tokens_topk(const uint16_t* logits, int64_t row_stride, int64_t n
  * is NULL.  Equal (seed, offset, q) reproduce a row's token, whatever the
  * other rows.  out_tokens int64 [n_rows]; out_logprobs fp32 [n_rows] or NULL.
  * workspace: qmi_lm_head_workspace_bytes(n_rows, vocab, top_k) bytes, 16-byte
- * aligned (per-row, per-128-entry-tile softmax pairs and, with top-k, each
+ * aligned (per-row softmax pairs over 32-, 64- or 128-entry slices of the
+ * vocabulary, by row count, and, with top-k, each
  * tile's four largest logits; no initial contents).  top_k above 64, or top-k
  * over a vocabulary above 262,144 entries, returns QMI_E_UNSUPPORTED (top-k
  * sampling from materialised logits: qmi_sample_tokens_topk).

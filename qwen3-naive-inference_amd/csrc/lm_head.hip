@@ -14,8 +14,9 @@
 // Kernel 1, lmhead_items: a work item (TVB vocabulary tiles of 128 rows, a
 // tile of MT hidden-state rows) computes its logits with
 // v_mfma_f32_16x16x32_bf16 and reduces them on the spot to one (max, sum of
-// exp2) pair per row and 128-row vocabulary tile in the log2 domain
-// (x * log2(e) / T); in target mode the lane holding a row's target also
+// exp2) pair per row and wave slice of the vocabulary (32, 64 or 128 entries
+// by configuration) in the log2 domain (x * log2(e) / T); in target mode the
+// lane holding a row's target also
 // writes that logit; in top-k mode every (row, tile) also gets its four
 // largest logits (value descending, index ascending) as packed keys.  The
 // grid is persistent (one or two workgroups per CU), each workgroup running a
@@ -39,12 +40,12 @@
 //     2.73 ms against 128-entry items staged through registers).
 //   * W (311 MB for Qwen3-0.6B) is read once from HBM per row tile; H comes
 //     from L2.
-// Kernel 2, lmhead_sample_rows: one workgroup per row combines the row's tile
+// Kernel 2, lmhead_sample_rows: one workgroup per row combines the row's
 // pairs into its log-sum-exp and draws the token by inverse transform
 // sampling with one Philox4x32-10 uniform per row: the first vocabulary index
-// whose cumulative probability exceeds u (tile prefix sums in fp64, then the
-// chosen tile's 128 logits recomputed by the same MFMA sequence as kernel 1,
-// so they are bit-identical to the values its pairs summarise).  This is an
+// whose cumulative probability exceeds u (pair prefix sums in fp64, then the
+// chosen slice's 32-128 logits recomputed by the same MFMA sequence as kernel
+// 1, so they are bit-identical to the values its pair summarises).  This is an
 // exact draw from softmax(x / T) and costs one random number per row instead
 // of one per vocabulary entry.
 // Kernel 2', lmhead_topk_rows: the k kept entries are found among the
@@ -190,7 +191,6 @@ __global__ __launch_bounds__(NW * 64) void lmhead_items(
   static_assert(WL >= 1 && HL >= 1 && TV % (8 * NW) == 0 && MT % (8 * NW) == 0, "loads");
   static_assert(NSTAGE >= 2 && NSTAGE * STAGE <= 160 * 1024, "LDS");
   __shared__ __align__(16) unsigned char lds[NSTAGE * STAGE];
-  __shared__ float2 red[WPT > 1 ? NVQ : 1][WPT > 1 ? MT : 1];
   __shared__ uint4 redk[WPT > 1 && TOPK ? NVQ : 1][WPT > 1 && TOPK ? MT : 1];
 
   const int tid = threadIdx.x;
@@ -200,6 +200,7 @@ __global__ __launch_bounds__(NW * 64) void lmhead_items(
   const int vq = wave % NVQ, rq = wave / NVQ;
   const int n_kc = hidden / kKC;
   const int n_vitems = (n_vtiles + TVB - 1) / TVB;
+  const int n_pairs = (vocab + VW - 1) / VW;  // (max, sum) pairs per row
   const int n_items = n_vitems * n_rtiles;
   // Item order.  With one row tile every item shares the hidden-state tile,
   // and a workgroup takes a contiguous range of items.  With several row
@@ -325,16 +326,18 @@ __global__ __launch_bounds__(NW * 64) void lmhead_items(
     }
   };
 
-  // Epilogue of an item: per row, (max, sum of exp2) over each 128-entry
-  // vocabulary tile; acc[vb][rb][e] holds vocabulary v0 + VW vq + 16 vb +
-  // 4 g4 + e of row r0 + 64 rq + 16 rb + l16.  Each logit is first rounded
-  // to bf16 (the reference's lm_head output).
+  // Epilogue of an item: per row, (max, sum of exp2) over each wave's VW
+  // entries of the vocabulary (pair v / VW; the top-k mode needs none);
+  // acc[vb][rb][e] holds vocabulary v0 + VW vq + 16 vb + 4 g4 + e of row
+  // r0 + 64 rq + 16 rb + l16.  Each logit is first rounded to bf16 (the
+  // reference's lm_head output).
   auto epilogue = [&](Pos it) __attribute__((always_inline)) {
     const int64_t v0 = (int64_t)it.vi * TV;
     const int64_t r0 = (int64_t)it.rt * MT;
     const int64_t vbase = v0 + VW * vq + 4 * g4;
     const int vt = (int)(v0 / kTV) + (VW * vq) / kTV;  // this wave's 128-row tile
     const int lbase = (VW * vq) % kTV + 4 * g4;        // its first entry within the tile
+    const int pidx = (int)(v0 / VW) + vq;              // this wave's (max, sum) pair
     // Only an item that reaches past the end of the vocabulary checks each
     // entry (a wave-uniform choice between two copies of the loop).
     const int vrel = vocab - (int)vbase;  // entries of this lane's columns that exist: j < vrel
@@ -377,39 +380,37 @@ __global__ __launch_bounds__(NW * 64) void lmhead_items(
             cand[row * (int64_t)n_vtiles + vt] = make_uint4(t.c0, t.c1, t.c2, t.c3);
         }
       }
-      // (max, sum of exp2) of x c2 (c2 > 0, so the maximum is taken on the
-      // logits and scaled once); entries past the vocabulary add nothing.
-      float mx = kNegBig;
+      if constexpr (!TOPK) {
+        // (max, sum of exp2) of x c2 (c2 > 0, so the maximum is taken on the
+        // logits and scaled once); entries past the vocabulary add nothing.
+        float mx = kNegBig;
 #pragma unroll
-      for (int vb = 0; vb < VB; ++vb)
+        for (int vb = 0; vb < VB; ++vb)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const bool ok = !check || 16 * vb + e < vrel;
-          mx = fmaxf(mx, ok ? acc[vb][rb][e] : kNegBig);
-        }
-      mx *= c2;
-      float sm = 0.f;
+          for (int e = 0; e < 4; ++e) {
+            const bool ok = !check || 16 * vb + e < vrel;
+            mx = fmaxf(mx, ok ? acc[vb][rb][e] : kNegBig);
+          }
+        mx *= c2;
+        float sm = 0.f;
 #pragma unroll
-      for (int vb = 0; vb < VB; ++vb)
+        for (int vb = 0; vb < VB; ++vb)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const bool ok = !check || 16 * vb + e < vrel;
-          const float p = fast_exp2(fmaf(acc[vb][rb][e], c2, -mx));
-          sm += ok ? p : 0.f;
-        }
-      LanePair pm = lane_pair16(mx), ps = lane_pair16(sm);
-      mx = pm.lo;
-      sm = ps.lo;
-      lse2_merge(mx, sm, pm.hi, ps.hi);
-      pm = lane_pair32(mx);
-      ps = lane_pair32(sm);
-      mx = pm.lo;
-      sm = ps.lo;
-      lse2_merge(mx, sm, pm.hi, ps.hi);
-      if constexpr (WPT > 1) {
-        if (g4 == 0) red[vq][row_l] = make_float2(mx, sm);
-      } else {
-        if (g4 == 0 && row < n_rows && vt < n_vtiles) part[row * (int64_t)n_vtiles + vt] = make_float2(mx, sm);
+          for (int e = 0; e < 4; ++e) {
+            const bool ok = !check || 16 * vb + e < vrel;
+            const float p = fast_exp2(fmaf(acc[vb][rb][e], c2, -mx));
+            sm += ok ? p : 0.f;
+          }
+        LanePair pm = lane_pair16(mx), ps = lane_pair16(sm);
+        mx = pm.lo;
+        sm = ps.lo;
+        lse2_merge(mx, sm, pm.hi, ps.hi);
+        pm = lane_pair32(mx);
+        ps = lane_pair32(sm);
+        mx = pm.lo;
+        sm = ps.lo;
+        lse2_merge(mx, sm, pm.hi, ps.hi);
+        if (g4 == 0 && row < n_rows && pidx < n_pairs) part[row * (int64_t)n_pairs + pidx] = make_float2(mx, sm);
       }
 #pragma unroll
       for (int vb = 0; vb < VB; ++vb) acc[vb][rb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -419,7 +420,7 @@ __global__ __launch_bounds__(NW * 64) void lmhead_items(
       rows(std::false_type{});
     else
       rows(std::true_type{});
-    if constexpr (WPT > 1) {
+    if constexpr (WPT > 1 && TOPK) {
       __syncthreads();
       // Waves WPT tj .. WPT tj + WPT - 1 hold the item's tile tj.
       for (int r = tid; r < MT; r += NW * 64) {
@@ -428,21 +429,14 @@ __global__ __launch_bounds__(NW * 64) void lmhead_items(
           for (int tj = 0; tj < TVB; ++tj) {
             const int vt = (int)(v0 / kTV) + tj;
             if (vt < n_vtiles) {
-              float2 a = red[WPT * tj][r];
+              const uint4 k0 = redk[WPT * tj][r];
+              Top4 t{k0.x, k0.y, k0.z, k0.w};
 #pragma unroll
-              for (int j = 1; j < WPT; ++j)
-                lse2_merge(a.x, a.y, red[WPT * tj + j][r].x, red[WPT * tj + j][r].y);
-              part[(r0 + r) * (int64_t)n_vtiles + vt] = a;
-              if constexpr (TOPK) {
-                const uint4 k0 = redk[WPT * tj][r];
-                Top4 t{k0.x, k0.y, k0.z, k0.w};
-#pragma unroll
-                for (int j = 1; j < WPT; ++j) {
-                  const uint4 kj = redk[WPT * tj + j][r];
-                  t.merge(Top4{kj.x, kj.y, kj.z, kj.w});
-                }
-                cand[(r0 + r) * (int64_t)n_vtiles + vt] = make_uint4(t.c0, t.c1, t.c2, t.c3);
+              for (int j = 1; j < WPT; ++j) {
+                const uint4 kj = redk[WPT * tj + j][r];
+                t.merge(Top4{kj.x, kj.y, kj.z, kj.w});
               }
+              cand[(r0 + r) * (int64_t)n_vtiles + vt] = make_uint4(t.c0, t.c1, t.c2, t.c3);
             }
           }
         }
@@ -572,18 +566,21 @@ __device__ __forceinline__ void load_hrow(const uint16_t* __restrict__ hr, int h
     *reinterpret_cast<uint4*>(hrow + k) = load_u4(hr + k);
 }
 
-// The bf16-rounded logits of vocabulary tile `tile` (entries 128 tile .. +128)
-// for the hidden-state row in LDS, into xs[128] (-inf past the vocabulary).
-// All 256 threads take part; wave i computes entries 32 i .. +32 with the
-// MFMA sequence of lmhead_items (the same operand layout, hidden elements in
-// the same order: 32 at a time, lane group g4 supplying elements 8 g4 .. +8
-// of each 32), every column of the B operand holding the row, so the values
-// are bit-identical to the ones lmhead_items reduced.
-__device__ __forceinline__ void tile_logits(const uint16_t* hrow, const uint16_t* __restrict__ w,
-                            int64_t w_stride, int vocab, int hidden, int tile, float* xs) {
+// The bf16-rounded logits of vocabulary entries first .. first + count
+// (count 32, 64 or 128) for the hidden-state row in LDS, into xs[count]
+// (-inf past the vocabulary).  Wave i computes entries first + 32 i .. +32
+// (waves past count skip) with the MFMA sequence of lmhead_items (the same
+// operand layout, hidden elements in the same order: 32 at a time, lane group
+// g4 supplying elements 8 g4 .. +8 of each 32; each 16-entry block
+// accumulates on its own), every column of the B operand holding the row, so
+// the values are bit-identical to the ones lmhead_items reduced.
+__device__ __forceinline__ void entry_logits(const uint16_t* hrow, const uint16_t* __restrict__ w,
+                                             int64_t w_stride, int vocab, int hidden, int64_t first,
+                                             int count, float* xs) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, g4 = lane >> 4;
-  const int64_t vw = (int64_t)tile * kTV + 32 * wave;
+  if (32 * wave >= count) return;  // wave-uniform
+  const int64_t vw = first + 32 * wave;
   const uint16_t* wr0 = w + (vw + l16 < vocab ? vw + l16 : (int64_t)vocab - 1) * w_stride + 8 * g4;
   const uint16_t* wr1 = w + (vw + 16 + l16 < vocab ? vw + 16 + l16 : (int64_t)vocab - 1) * w_stride + 8 * g4;
   f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
@@ -635,7 +632,7 @@ __device__ __forceinline__ void tile_logits(const uint16_t* hrow, const uint16_t
 }
 
 __global__ __launch_bounds__(kRowThreads) void lmhead_sample_rows(
-    const float2* __restrict__ part, int n_vtiles, const uint16_t* __restrict__ h,
+    const float2* __restrict__ part, int n_pairs, int sub, const uint16_t* __restrict__ h,
     int64_t h_stride, const uint16_t* __restrict__ w, int64_t w_stride, int vocab, int hidden,
     float c2, uint32_t seed_lo, uint32_t seed_hi, uint32_t off_lo, uint32_t off_hi,
     const uint64_t* __restrict__ row_ctr, int64_t* __restrict__ out_tok, float* __restrict__ out_lp) {
@@ -647,13 +644,14 @@ __global__ __launch_bounds__(kRowThreads) void lmhead_sample_rows(
   __shared__ __align__(16) uint16_t hrow[kMaxHidden];
   const int tid = threadIdx.x;
   const int row = blockIdx.x;
-  const float2* pr = part + (int64_t)row * n_vtiles;
-  const int cpt = (n_vtiles + kRowThreads - 1) / kRowThreads;
-  const int lo = min(n_vtiles, tid * cpt), hi = min(n_vtiles, lo + cpt);
+  // The row's (max, sum) pairs, one per `sub` vocabulary entries.
+  const float2* pr = part + (int64_t)row * n_pairs;
+  const int cpt = (n_pairs + kRowThreads - 1) / kRowThreads;
+  const int lo = min(n_pairs, tid * cpt), hi = min(n_pairs, lo + cpt);
   // A thread's pairs are read once into registers when they fit (up to
-  // 2,048 tiles), in flight together with the hidden-state row; entries past
+  // 5,120 pairs), in flight together with the hidden-state row; entries past
   // its chunk hold (-big, 0), which add exactly zero to the fp64 sums.
-  constexpr int kPR = 8;
+  constexpr int kPR = 20;
   const bool regs = cpt <= kPR;
   float2 pv[kPR];
   if (regs) {
@@ -675,7 +673,7 @@ __global__ __launch_bounds__(kRowThreads) void lmhead_sample_rows(
     own = acc;
     excl = block_excl_scan256(acc, smd, &L.s);
   } else {
-    L = row_lse(pr, n_vtiles, cpt, &own, &excl, smf, smd);
+    L = row_lse(pr, n_pairs, cpt, &own, &excl, smf, smd);
   }
   const double target = u * L.s;
 
@@ -713,28 +711,29 @@ __global__ __launch_bounds__(kRowThreads) void lmhead_sample_rows(
   }
   __syncthreads();
   if (sel_tile < 0) {
-    // u * S rounded up to S: the last tile with mass, at its last entry.
+    // u * S rounded up to S: the last pair with mass, at its last entry.
     if (tid == 0) {
-      int t = n_vtiles - 1;
+      int t = n_pairs - 1;
       while (t > 0 && !(pr[t].y * fast_exp2(pr[t].x - L.m2) > 0.f)) --t;
       sel_tile = t;
       sel_resid = 1e300;
     }
     __syncthreads();
   }
-  const int t_sel = sel_tile;
-  tile_logits(hrow, w, w_stride, vocab, hidden, t_sel, xs);
+  const int64_t first = (int64_t)sel_tile * sub;
+  entry_logits(hrow, w, w_stride, vocab, hidden, first, sub, xs);
   __syncthreads();
-  // Within the tile: the first column whose cumulative mass exceeds the
-  // residual (wave 0, two columns per lane, fixed-order scan).
+  // Within the pair's entries: the first whose cumulative mass exceeds the
+  // residual (wave 0, two entries per lane, fixed-order scan).
   if (tid < 64) {
     const double resid = sel_resid;
-    const float x0 = xs[2 * tid], x1 = xs[2 * tid + 1];
+    const float x0 = 2 * tid < sub ? xs[2 * tid] : -INFINITY;
+    const float x1 = 2 * tid + 1 < sub ? xs[2 * tid + 1] : -INFINITY;
     const double p0 = x0 == -INFINITY ? 0.0 : (double)fast_exp2(x0 * c2 - L.m2);
     const double p1 = x1 == -INFINITY ? 0.0 : (double)fast_exp2(x1 * c2 - L.m2);
     const double inc = wave_scan_f64(p0 + p1);
     const double before = inc - (p0 + p1);
-    int cand = kTV;
+    int cand = sub;
     if (resid < before + p0) cand = 2 * tid;
     else if (resid < inc) cand = 2 * tid + 1;
     int last = p1 > 0.0 ? 2 * tid + 1 : (p0 > 0.0 ? 2 * tid : -1);
@@ -744,8 +743,8 @@ __global__ __launch_bounds__(kRowThreads) void lmhead_sample_rows(
       last = max(last, __shfl_xor(last, m, 64));
     }
     if (tid == 0) {
-      const int pick = cand < kTV ? cand : (last >= 0 ? last : 0);
-      out_tok[row] = (int64_t)t_sel * kTV + pick;
+      const int pick = cand < sub ? cand : (last >= 0 ? last : 0);
+      out_tok[row] = first + pick;
       if (out_lp) {
         const double lse2 = (double)L.m2 + log2(L.s);
         out_lp[row] = (float)(((double)(xs[pick] * c2) - lse2) * (double)kLn2);
@@ -925,7 +924,8 @@ __global__ __launch_bounds__(kRowThreads) void lmhead_topk_rows(
     // Saturated tiles: all 128 logits, then the selection once more.
     load_hrow(h + (int64_t)row * h_stride, hidden, hrow);
     __syncthreads();
-    for (int j = 0; j < ns; ++j) tile_logits(hrow, w, w_stride, vocab, hidden, sat_tile[j], sat_x[j]);
+    for (int j = 0; j < ns; ++j)
+      entry_logits(hrow, w, w_stride, vocab, hidden, (int64_t)sat_tile[j] * kTV, kTV, sat_x[j]);
     __syncthreads();
     select();
   }
@@ -1024,15 +1024,15 @@ __global__ __launch_bounds__(kRowThreads) void lmhead_topk_rows(
 }
 
 __global__ __launch_bounds__(kRowThreads) void lmhead_logprob_rows(
-    const float2* __restrict__ part, int n_vtiles, const float* __restrict__ tgt_logit,
+    const float2* __restrict__ part, int n_pairs, const float* __restrict__ tgt_logit,
     const int64_t* __restrict__ tgt, int64_t tgt_stride, int vocab, float c2,
     float* __restrict__ out_lp, float* __restrict__ out_lse) {
   __shared__ float smf[4];
   __shared__ double smd[5];
   const int row = blockIdx.x;
-  const int cpt = (n_vtiles + kRowThreads - 1) / kRowThreads;
+  const int cpt = (n_pairs + kRowThreads - 1) / kRowThreads;
   double own, excl;
-  const RowLse L = row_lse(part + (int64_t)row * n_vtiles, n_vtiles, cpt, &own, &excl, smf, smd);
+  const RowLse L = row_lse(part + (int64_t)row * n_pairs, n_pairs, cpt, &own, &excl, smf, smd);
   if (threadIdx.x == 0) {
     const double lse = ((double)L.m2 + log2(L.s)) * (double)kLn2;  // of x * c2 / log2(e)
     if (out_lse) out_lse[row] = (float)lse;
@@ -1056,17 +1056,27 @@ struct LmWs {
 inline int64_t n_vtiles_of(int64_t vocab) { return (vocab + kTV - 1) / kTV; }
 inline int64_t round256(int64_t b) { return (b + 255) & ~(int64_t)255; }
 
-// Workspace: (max, sum) pairs [rows, tiles] fp32x2, target logits [rows]
+// Vocabulary entries per (max, sum) pair: what one wave of the item kernel
+// covers in the configuration launch_tiles picks for n_rows (items of
+// 128 x 64 with 4 waves, 256 x 128 with 8 waves of 64 x 64, 256 x 256 with
+// 8 waves of 128 x 64).
+inline int pair_entries(int64_t n_rows) { return n_rows <= 64 ? 32 : n_rows <= 256 ? 64 : 128; }
+inline int64_t n_pairs_of(int64_t n_rows, int64_t vocab) {
+  const int e = pair_entries(n_rows);
+  return (vocab + e - 1) / e;
+}
+
+// Workspace: (max, sum) pairs [rows, pairs] fp32x2, target logits [rows]
 // fp32, then with top-k the candidate keys [rows, tiles] uint32x4.
 inline int64_t ws_bytes(int64_t n_rows, int64_t vocab, bool topk) {
-  const int64_t nt = n_vtiles_of(vocab);
-  const int64_t b = round256(n_rows * nt * (int64_t)sizeof(float2)) + round256(n_rows * (int64_t)sizeof(float));
-  return topk ? b + n_rows * nt * (int64_t)sizeof(uint4) : b;
+  const int64_t np = n_pairs_of(n_rows, vocab);
+  const int64_t b = round256(n_rows * np * (int64_t)sizeof(float2)) + round256(n_rows * (int64_t)sizeof(float));
+  return topk ? b + n_rows * n_vtiles_of(vocab) * (int64_t)sizeof(uint4) : b;
 }
 
 inline LmWs ws_layout(void* ws, int64_t n_rows, int64_t vocab) {
-  const int64_t nt = n_vtiles_of(vocab);
-  const int64_t p = round256(n_rows * nt * (int64_t)sizeof(float2));
+  const int64_t np = n_pairs_of(n_rows, vocab);
+  const int64_t p = round256(n_rows * np * (int64_t)sizeof(float2));
   const int64_t t = round256(n_rows * (int64_t)sizeof(float));
   char* base = static_cast<char*>(ws);
   return {reinterpret_cast<float2*>(base), reinterpret_cast<float*>(base + p),
@@ -1100,6 +1110,8 @@ int launch_tiles(const uint16_t* h, int64_t h_stride, int64_t n_rows, const uint
   // there are fewer items.
 #define QMI_LMI(MT, NW, NS, TVB, PER_CU, TOPK)                                                     \
   do {                                                                                            \
+    /* the kernel's (max, sum) pairs cover one wave's entries: the layout's width */            \
+    if ((kTV * TVB) / (NW / (MT / 64)) != pair_entries(n_rows)) return QMI_E_UNSUPPORTED;        \
     const int nrt = (int)((n_rows + MT - 1) / MT);                                                \
     const int64_t items = (int64_t)((nvt + TVB - 1) / TVB) * nrt;                                 \
     const int64_t grid = std::min<int64_t>(items, (int64_t)device_cu_count() * PER_CU);           \
@@ -1171,7 +1183,8 @@ extern "C" int qmi_lm_head_sample(const uint16_t* hidden_states, int64_t h_strid
                        row_counters, out_tokens, out_logprobs);
   else
     hipLaunchKernelGGL(lmhead_sample_rows, dim3((unsigned)n_rows), dim3(kRowThreads), 0, s,
-                       ws.part, (int)n_vtiles_of(vocab), hidden_states, h_stride, weight, w_stride,
+                       ws.part, (int)n_pairs_of(n_rows, vocab), pair_entries(n_rows), hidden_states,
+                       h_stride, weight, w_stride,
                        (int)vocab, (int)hidden, c2, (uint32_t)seed, (uint32_t)(seed >> 32),
                        (uint32_t)offset, (uint32_t)(offset >> 32), row_counters, out_tokens,
                        out_logprobs);
@@ -1194,7 +1207,7 @@ extern "C" int qmi_lm_head_logprob(const uint16_t* hidden_states, int64_t h_stri
                     targets, target_stride, false, ws, s);
   if (st != QMI_OK) return st;
   hipLaunchKernelGGL(lmhead_logprob_rows, dim3((unsigned)n_rows), dim3(kRowThreads), 0, s, ws.part,
-                     (int)n_vtiles_of(vocab), ws.tgt_logit, targets, target_stride, (int)vocab,
+                     (int)n_pairs_of(n_rows, vocab), ws.tgt_logit, targets, target_stride, (int)vocab,
                      kLog2e, out_logprobs, out_lse);
   QMI_RETURN_LAUNCH_STATUS();
 }
