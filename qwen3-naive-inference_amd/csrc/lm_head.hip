@@ -15,10 +15,9 @@
 // tile of MT hidden-state rows) computes its logits with
 // v_mfma_f32_16x16x32_bf16 and reduces them on the spot to one (max, sum of
 // exp2) pair per row and wave slice of the vocabulary (32, 64 or 128 entries
-// by configuration) in the log2 domain (x * log2(e) / T); in target mode the
-// lane holding a row's target also
-// writes that logit; in top-k mode every (row, tile) also gets its four
-// largest logits (value descending, index ascending) as packed keys.  The
+// by configuration) in the log2 domain (x * log2(e) / T), or, in top-k mode,
+// to every (row, tile)'s four largest logits (value descending, index
+// ascending) as packed keys.  The
 // grid is persistent (one or two workgroups per CU), each workgroup running a
 // contiguous range of items as one pipeline of (item, 64-hidden chunk) steps,
 // so the loads never drain at item boundaries.  Operands are computed
@@ -53,7 +52,10 @@
 // index), then drawn from by inverse transform sampling in vocabulary order.
 // The top k of a row lie in its candidates unless some tile holds four or
 // more of them; such a tile is recomputed in full and the selection repeated.
-// Kernel 2'', lmhead_logprob_rows: lse and lp = x[target] - lse per row.
+// Kernel 2'', lmhead_logprob_rows: lse and lp = x[target] - lse per row, the
+// target's logit recomputed from its weight row by the same MFMA sequence
+// (so bit-identical; the item kernel then loads no target ids, whose waits
+// would drain its load pipeline once per item).
 #include <algorithm>
 #include <type_traits>
 
@@ -174,8 +176,7 @@ template <int MT, int NW, int NSTAGE, int TVB, bool TOPK, bool XO>
 __global__ __launch_bounds__(NW * 64) void lmhead_items(
     const uint16_t* __restrict__ h, int64_t h_stride, int n_rows,
     const uint16_t* __restrict__ w, int64_t w_stride, int vocab, int hidden, float c2,
-    const int64_t* __restrict__ tgt, int64_t tgt_stride, int n_vtiles, int n_rtiles,
-    float2* __restrict__ part, float* __restrict__ tgt_logit, uint4* __restrict__ cand) {
+    int n_vtiles, int n_rtiles, float2* __restrict__ part, uint4* __restrict__ cand) {
   constexpr int TV = kTV * TVB;
   constexpr int NRQ = MT / 64;       // row blocks of 64
   constexpr int NVQ = NW / NRQ;      // waves per row block
@@ -313,19 +314,6 @@ __global__ __launch_bounds__(NW * 64) void lmhead_items(
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) acc[vb][rb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  // Target vocabulary index of each row block's row for this lane, -1 when
-  // out of range (such a row's log-prob is NaN, set by the row kernel).
-  int tgt_id[4] = {-1, -1, -1, -1};
-  auto load_targets = [&](Pos it) __attribute__((always_inline)) {
-    const int r0 = it.rt * MT;
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-      const int row = r0 + 64 * rq + 16 * rb + l16;
-      const int64_t t = tgt[(int64_t)(row < n_rows ? row : n_rows - 1) * tgt_stride];
-      tgt_id[rb] = t >= 0 && t < vocab ? (int)t : -1;
-    }
-  };
-
   // Epilogue of an item: per row, (max, sum of exp2) over each wave's VW
   // entries of the vocabulary (pair v / VW; the top-k mode needs none);
   // acc[vb][rb][e] holds vocabulary v0 + VW vq + 16 vb + 4 g4 + e of row
@@ -350,20 +338,6 @@ __global__ __launch_bounds__(NW * 64) void lmhead_items(
       for (int vb = 0; vb < VB; ++vb)
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc[vb][rb][e] = bf16_round(acc[vb][rb][e]);
-      if (tgt) {  // the target's logit, by the lane holding it
-        const int tl = tgt_id[rb] - (int)vbase;  // 16 vb + e if this lane holds it
-        const bool mine = row < n_rows && tgt_id[rb] >= 0 && tl >= 0 && tl < VW && (tl & 12) == 0;
-        // Few waves hold a target in a given row block (16 rows x VW entries of
-        // the vocabulary): the selection runs only in those, by conditional moves.
-        if (__ballot(mine) != 0ull) {
-          float v = 0.f;
-#pragma unroll
-          for (int vb = 0; vb < VB; ++vb)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v = tl == 16 * vb + e ? acc[vb][rb][e] : v;
-          if (mine) tgt_logit[row] = v;
-        }
-      }
       if constexpr (TOPK) {
         Top4 t{0u, 0u, 0u, 0u};
 #pragma unroll
@@ -455,7 +429,6 @@ __global__ __launch_bounds__(NW * 64) void lmhead_items(
   asm volatile("s_waitcnt vmcnt(%0)" ::"i"((NSTAGE - 2) * LPW) : "memory");
   __syncthreads();
   for (int st = 0; st < n_steps; ++st) {
-    if (tgt && kc == 0) load_targets(it);
     issue(stage == 0 ? NSTAGE - 1 : stage - 1);
     const unsigned char* base = lds + stage * STAGE;
 #pragma unroll
@@ -1023,25 +996,61 @@ __global__ __launch_bounds__(kRowThreads) void lmhead_topk_rows(
   }
 }
 
+// The bf16-rounded logit of one vocabulary entry for one hidden-state row
+// (weight row wr and hidden row hr staged in LDS), by one wave: the MFMA
+// sequence of lmhead_items with the entry's weight row in all 16 rows of the
+// A operand and the hidden row in all 16 columns of B.  Every output element
+// is then the same dot product, summed in the item kernel's order (32 hidden
+// elements per MFMA, in increasing order), so the value is bit-identical to
+// the one that entered the entry's (max, sum) pair.
+__device__ __forceinline__ float entry_logit(const uint16_t* hr, const uint16_t* wr, int hidden) {
+  const int g4 = (threadIdx.x & 63) >> 4;
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  for (int k = 8 * g4; k < hidden; k += 64) {  // hidden is a multiple of 64
+    const bf16x8_t a0 = as_bf16x8(*reinterpret_cast<const uint4*>(wr + k));
+    const bf16x8_t a1 = as_bf16x8(*reinterpret_cast<const uint4*>(wr + k + 32));
+    const bf16x8_t b0 = as_bf16x8(*reinterpret_cast<const uint4*>(hr + k));
+    const bf16x8_t b1 = as_bf16x8(*reinterpret_cast<const uint4*>(hr + k + 32));
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, acc, 0, 0, 0);
+  }
+  return bf16_round(acc[0]);
+}
+
+// lse and lp = x[target] - lse per row: the lse from the row's pairs, the
+// target's logit recomputed (entry_logit) from its weight row and the hidden
+// row, both copied into LDS by the whole workgroup (one round trip, beside
+// the pair reads).  A target outside the vocabulary has no logit: NaN (the
+// reference's gather would raise).  Dynamic LDS: 4 * hidden bytes.
 __global__ __launch_bounds__(kRowThreads) void lmhead_logprob_rows(
-    const float2* __restrict__ part, int n_pairs, const float* __restrict__ tgt_logit,
-    const int64_t* __restrict__ tgt, int64_t tgt_stride, int vocab, float c2,
+    const float2* __restrict__ part, int n_pairs, const uint16_t* __restrict__ h,
+    int64_t h_stride, const uint16_t* __restrict__ w, int64_t w_stride,
+    const int64_t* __restrict__ tgt, int64_t tgt_stride, int vocab, int hidden, float c2,
     float* __restrict__ out_lp, float* __restrict__ out_lse) {
   __shared__ float smf[4];
   __shared__ double smd[5];
+  extern __shared__ __align__(16) uint16_t rows_lds[];  // [hidden] weight row, [hidden] hidden row
   const int row = blockIdx.x;
+  const int64_t t = tgt[(int64_t)row * tgt_stride];
+  const bool valid = t >= 0 && t < vocab;  // uniform over the workgroup
+  if (valid) {
+    const uint16_t* wr = w + t * w_stride;
+    const uint16_t* hr = h + (int64_t)row * h_stride;
+    for (int k = 8 * (int)threadIdx.x; k < hidden; k += 8 * kRowThreads) {
+      *reinterpret_cast<uint4*>(rows_lds + k) = load_u4(wr + k);
+      *reinterpret_cast<uint4*>(rows_lds + hidden + k) = load_u4(hr + k);
+    }
+  }
   const int cpt = (n_pairs + kRowThreads - 1) / kRowThreads;
   double own, excl;
   const RowLse L = row_lse(part + (int64_t)row * n_pairs, n_pairs, cpt, &own, &excl, smf, smd);
+  __syncthreads();  // the rows in LDS
+  float x = 0.f;
+  if (valid && threadIdx.x < 64) x = entry_logit(rows_lds + hidden, rows_lds, hidden);
   if (threadIdx.x == 0) {
     const double lse = ((double)L.m2 + log2(L.s)) * (double)kLn2;  // of x * c2 / log2(e)
     if (out_lse) out_lse[row] = (float)lse;
-    const int64_t t = tgt[(int64_t)row * tgt_stride];
-    // A target outside the vocabulary has no logit: NaN (the reference's
-    // gather would raise).
-    out_lp[row] = (t < 0 || t >= vocab)
-                      ? __builtin_nanf("")
-                      : (float)((double)tgt_logit[row] * (double)c2 * (double)kLn2 - lse);
+    out_lp[row] = valid ? (float)((double)x * (double)c2 * (double)kLn2 - lse) : __builtin_nanf("");
   }
 }
 
@@ -1049,7 +1058,6 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 struct LmWs {
   float2* part;
-  float* tgt_logit;
   uint4* cand;
 };
 
@@ -1066,21 +1074,19 @@ inline int64_t n_pairs_of(int64_t n_rows, int64_t vocab) {
   return (vocab + e - 1) / e;
 }
 
-// Workspace: (max, sum) pairs [rows, pairs] fp32x2, target logits [rows]
-// fp32, then with top-k the candidate keys [rows, tiles] uint32x4.
+// Workspace: (max, sum) pairs [rows, pairs] fp32x2, then with top-k the
+// candidate keys [rows, tiles] uint32x4.
 inline int64_t ws_bytes(int64_t n_rows, int64_t vocab, bool topk) {
   const int64_t np = n_pairs_of(n_rows, vocab);
-  const int64_t b = round256(n_rows * np * (int64_t)sizeof(float2)) + round256(n_rows * (int64_t)sizeof(float));
+  const int64_t b = round256(n_rows * np * (int64_t)sizeof(float2));
   return topk ? b + n_rows * n_vtiles_of(vocab) * (int64_t)sizeof(uint4) : b;
 }
 
 inline LmWs ws_layout(void* ws, int64_t n_rows, int64_t vocab) {
   const int64_t np = n_pairs_of(n_rows, vocab);
   const int64_t p = round256(n_rows * np * (int64_t)sizeof(float2));
-  const int64_t t = round256(n_rows * (int64_t)sizeof(float));
   char* base = static_cast<char*>(ws);
-  return {reinterpret_cast<float2*>(base), reinterpret_cast<float*>(base + p),
-          reinterpret_cast<uint4*>(base + p + t)};
+  return {reinterpret_cast<float2*>(base), reinterpret_cast<uint4*>(base + p)};
 }
 
 int check_args(const uint16_t* h, int64_t h_stride, int64_t n_rows, const uint16_t* w,
@@ -1098,8 +1104,8 @@ int check_args(const uint16_t* h, int64_t h_stride, int64_t n_rows, const uint16
 }
 
 int launch_tiles(const uint16_t* h, int64_t h_stride, int64_t n_rows, const uint16_t* w,
-                 int64_t w_stride, int64_t vocab, int64_t hidden, float c2, const int64_t* tgt,
-                 int64_t tgt_stride, bool topk, const LmWs& ws, hipStream_t s) {
+                 int64_t w_stride, int64_t vocab, int64_t hidden, float c2, bool topk,
+                 const LmWs& ws, hipStream_t s) {
   const int nvt = (int)n_vtiles_of(vocab);
   // Up to 64 rows: items of 128 x 64, 4 waves, three LDS stages, two 74 KB
   // workgroups per CU.  Up to 256 rows: items of 256 x 128 (two row tiles at
@@ -1118,13 +1124,11 @@ int launch_tiles(const uint16_t* h, int64_t h_stride, int64_t n_rows, const uint
     if (nrt > 1 && grid % 8 == 0 && grid >= 64)                                                   \
       hipLaunchKernelGGL((lmhead_items<MT, NW, NS, TVB, TOPK, true>), dim3((unsigned)grid),       \
                          dim3(NW * 64), 0, s, h, h_stride, (int)n_rows, w, w_stride, (int)vocab,  \
-                         (int)hidden, c2, tgt, tgt_stride, nvt, nrt, ws.part, ws.tgt_logit,       \
-                         ws.cand);                                                                \
+                         (int)hidden, c2, nvt, nrt, ws.part, ws.cand);                            \
     else                                                                                          \
       hipLaunchKernelGGL((lmhead_items<MT, NW, NS, TVB, TOPK, false>), dim3((unsigned)grid),      \
                          dim3(NW * 64), 0, s, h, h_stride, (int)n_rows, w, w_stride, (int)vocab,  \
-                         (int)hidden, c2, tgt, tgt_stride, nvt, nrt, ws.part, ws.tgt_logit,       \
-                         ws.cand);                                                                \
+                         (int)hidden, c2, nvt, nrt, ws.part, ws.cand);                            \
   } while (0)
   if (n_rows <= 64) {
     if (topk)
@@ -1172,8 +1176,8 @@ extern "C" int qmi_lm_head_sample(const uint16_t* hidden_states, int64_t h_strid
   const float c2 = kLog2e / temperature;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const LmWs ws = ws_layout(workspace, n_rows, vocab);
-  st = launch_tiles(hidden_states, h_stride, n_rows, weight, w_stride, vocab, hidden, c2, nullptr,
-                    0, topk, ws, s);
+  st = launch_tiles(hidden_states, h_stride, n_rows, weight, w_stride, vocab, hidden, c2, topk, ws,
+                    s);
   if (st != QMI_OK) return st;
   if (topk)
     hipLaunchKernelGGL(lmhead_topk_rows, dim3((unsigned)n_rows), dim3(kRowThreads), 0, s, ws.cand,
@@ -1203,11 +1207,12 @@ extern "C" int qmi_lm_head_logprob(const uint16_t* hidden_states, int64_t h_stri
   if (!targets || !out_logprobs) return QMI_E_NULL_POINTER;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const LmWs ws = ws_layout(workspace, n_rows, vocab);
-  st = launch_tiles(hidden_states, h_stride, n_rows, weight, w_stride, vocab, hidden, kLog2e,
-                    targets, target_stride, false, ws, s);
+  st = launch_tiles(hidden_states, h_stride, n_rows, weight, w_stride, vocab, hidden, kLog2e, false,
+                    ws, s);
   if (st != QMI_OK) return st;
-  hipLaunchKernelGGL(lmhead_logprob_rows, dim3((unsigned)n_rows), dim3(kRowThreads), 0, s, ws.part,
-                     (int)n_pairs_of(n_rows, vocab), ws.tgt_logit, targets, target_stride, (int)vocab,
-                     kLog2e, out_logprobs, out_lse);
+  hipLaunchKernelGGL(lmhead_logprob_rows, dim3((unsigned)n_rows), dim3(kRowThreads),
+                     (unsigned)(4 * hidden), s, ws.part,
+                     (int)n_pairs_of(n_rows, vocab), hidden_states, h_stride, weight, w_stride,
+                     targets, target_stride, (int)vocab, (int)hidden, kLog2e, out_logprobs, out_lse);
   QMI_RETURN_LAUNCH_STATUS();
 }

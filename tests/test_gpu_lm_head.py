@@ -142,6 +142,19 @@ def test_lm_head_logprob_out_of_range_target_is_nan(pkg, gpu):
     assert _lp_err(lp[ok], xr[ok], lo[ok], hi[ok], tgt.cpu()[ok], ref_lse[ok]).max() <= LP_TOL
 
 
+def test_lm_head_logprob_widest_hidden(pkg, gpu):
+    """Hidden size 16,384 (the largest the C ABI takes): the log-prob row kernel
+    stages the target's weight row and the hidden row (64 KB) in LDS."""
+    h, w, hg, wg = _inputs(gpu, 3, 300, hidden=16384, w_std=0.01, seed=11)
+    tgt = torch.tensor([0, 299, 150], device=gpu)
+    lp, lse = pkg.kernels.lm_head_logprob(hg, wg, tgt)
+    torch.cuda.synchronize()
+    xr, lo, hi = _logits_bf16(h, w)
+    ref_lse = torch.logsumexp(xr, -1)
+    assert _lp_err(lp.cpu(), xr, lo, hi, tgt.cpu(), ref_lse).max().item() <= LP_TOL
+    assert _rel(lse.cpu(), ref_lse) <= LP_TOL
+
+
 @pytest.mark.parametrize("n,vocab,temp", [(1, 2085, 1.0), (64, 151936, 1.0), (64, 151936, 0.6),
                                           (130, 2085, 1.0), (256, 151936, 1.0), (300, 5000, 0.8)])
 def test_lm_head_sample_matches_oracle(pkg, gpu, n, vocab, temp):
