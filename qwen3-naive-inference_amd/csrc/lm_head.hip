@@ -355,8 +355,11 @@ __global__ __launch_bounds__(NW * 64) void lmhead_items(
         }
       }
       if constexpr (!TOPK) {
-        // (max, sum of exp2) of x c2 (c2 > 0, so the maximum is taken on the
-        // logits and scaled once); entries past the vocabulary add nothing.
+        // (max, sum of exp2) of x c2 over the wave's slice of the row: the
+        // maximum over the four lanes holding the row first (c2 > 0, so it is
+        // taken on the logits and scaled once), then every lane's terms
+        // against it and one cross-lane sum; entries past the vocabulary add
+        // nothing.
         float mx = kNegBig;
 #pragma unroll
         for (int vb = 0; vb < VB; ++vb)
@@ -365,7 +368,7 @@ __global__ __launch_bounds__(NW * 64) void lmhead_items(
             const bool ok = !check || 16 * vb + e < vrel;
             mx = fmaxf(mx, ok ? acc[vb][rb][e] : kNegBig);
           }
-        mx *= c2;
+        mx = rows4_max(mx) * c2;
         float sm = 0.f;
 #pragma unroll
         for (int vb = 0; vb < VB; ++vb)
@@ -375,15 +378,7 @@ __global__ __launch_bounds__(NW * 64) void lmhead_items(
             const float p = fast_exp2(fmaf(acc[vb][rb][e], c2, -mx));
             sm += ok ? p : 0.f;
           }
-        LanePair pm = lane_pair16(mx), ps = lane_pair16(sm);
-        mx = pm.lo;
-        sm = ps.lo;
-        lse2_merge(mx, sm, pm.hi, ps.hi);
-        pm = lane_pair32(mx);
-        ps = lane_pair32(sm);
-        mx = pm.lo;
-        sm = ps.lo;
-        lse2_merge(mx, sm, pm.hi, ps.hi);
+        sm = rows4_sum(sm);
         if (g4 == 0 && row < n_rows && pidx < n_pairs) part[row * (int64_t)n_pairs + pidx] = make_float2(mx, sm);
       }
 #pragma unroll
