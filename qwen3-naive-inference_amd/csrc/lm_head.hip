@@ -17,10 +17,10 @@
 // exp2) pair per row and wave slice of the vocabulary (32, 64 or 128 entries
 // by configuration) in the log2 domain (x * log2(e) / T), or, in top-k mode,
 // to every (row, tile)'s four largest logits (value descending, index
-// ascending) as packed keys.  The
-// grid is persistent (one or two workgroups per CU), each workgroup running a
-// contiguous range of items as one pipeline of (item, 64-hidden chunk) steps,
-// so the loads never drain at item boundaries.  Operands are computed
+// ascending) as packed keys.  The grid is persistent (one or two workgroups
+// per CU), each workgroup running a contiguous range of items as one
+// pipeline of (item, 64-hidden chunk) steps, so the loads never drain at
+// item boundaries.  Operands are computed
 // transposed, S^T = W H^T: A = 16 vocabulary rows x 32 hidden of W, B = H^T
 // (32 hidden x 16 rows), so both operands are 16-byte row pieces and each
 // lane's accumulators hold 4 consecutive vocabulary entries of one row.
@@ -164,9 +164,9 @@ __device__ __forceinline__ void lds_load16(const void* gbase, uint32_t voff, uin
 // vocabulary tiles of 128 rows (TV = 128 TVB) x MT hidden-state rows; W and
 // H chunks go from global memory straight into NSTAGE LDS stages (no
 // register staging, no LDS write instructions), loads issued NSTAGE - 1
-// steps ahead.  Wave (vq, rq) owns vocabulary rows VW vq .. +VW (VW = 128
-// when TVB = NVQ: one wave per 128-row tile, whose (max, sum) pairs it
-// writes itself) and hidden-state rows 64 rq .. +64.  Rows past the
+// steps ahead.  Wave (vq, rq) owns vocabulary rows VW vq .. +VW and
+// hidden-state rows 64 rq .. +64, and writes the (max, sum) pair of its VW
+// entries for each of its rows (pair v0 / VW + vq).  Rows past the
 // vocabulary or the batch load the last valid row (their results are
 // masked or not written).  Per-item H traffic is what bounds this kernel at
 // a few hundred rows and above (each item re-reads its MT x hidden rows from
