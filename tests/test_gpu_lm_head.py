@@ -199,7 +199,9 @@ def _topk_case(kind, n, vocab, seed):
 @pytest.mark.parametrize("kind,n,vocab,k,temp", [
     ("plain", 1, 2085, 20, 1.0), ("plain", 64, 151936, 20, 0.6), ("plain", 256, 151936, 20, 1.0),
     ("plain", 100, 4096, 64, 0.8), ("plain", 37, 3000, 1, 1.0), ("plain", 70, 300, 64, 1.0),
+    ("plain", 300, 2085, 20, 0.8),
     ("clustered", 8, 151936, 20, 1.0), ("clustered", 80, 5000, 32, 0.7),
+    ("clustered", 260, 3000, 20, 1.0),
     ("ties16", 4, 4096, 20, 1.0), ("ties16", 90, 4096, 37, 0.9)])
 def test_lm_head_topk_matches_oracle(pkg, gpu, kind, n, vocab, k, temp):
     """Fused lm_head + top-k sampling (the reference default k = 20) against
