@@ -514,7 +514,9 @@ int qmi_sample_tokens_topk(const uint16_t* logits, int64_t row_stride, int64_t n
  * vocabulary, by row count, and, with top-k, each
  * tile's four largest logits; no initial contents).  top_k above 64, or top-k
  * over a vocabulary above 262,144 entries, returns QMI_E_UNSUPPORTED (top-k
- * sampling from materialised logits: qmi_sample_tokens_topk).
+ * sampling from materialised logits: qmi_sample_tokens_topk), as does a call
+ * whose ceil(vocab / 128) x ceil(n_rows / 64) x hidden / 64 exceeds 2^31 - 1
+ * (about 7 million rows at Qwen3-0.6B's shape: split such a call by rows).
  */
 int64_t qmi_lm_head_workspace_bytes(int64_t n_rows, int64_t vocab, int64_t top_k);
 

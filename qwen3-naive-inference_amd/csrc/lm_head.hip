@@ -1091,6 +1091,10 @@ int check_args(const uint16_t* h, int64_t h_stride, int64_t n_rows, const uint16
   if (!h || !w || !ws) return QMI_E_NULL_POINTER;
   if (hidden % kKC != 0 || hidden > kMaxHidden) return QMI_E_UNSUPPORTED;
   if (vocab > 0x7fffffffLL - kTV || n_rows > 0x7fffffffLL) return QMI_E_UNSUPPORTED;
+  // The item kernel counts its work items and (item, chunk) steps in 32-bit
+  // integers: at most n_vtiles x ceil(n_rows / 64) items of hidden / 64 steps.
+  if (n_vtiles_of(vocab) * ((n_rows + 63) / 64) * (hidden / kKC) > 0x7fffffffLL)
+    return QMI_E_UNSUPPORTED;
   if (h_stride < hidden || w_stride < hidden) return QMI_E_BAD_STRIDE;
   if (h_stride % 8 || w_stride % 8 || !aligned16(h) || !aligned16(w) || !aligned16(ws))
     return QMI_E_BAD_STRIDE;

@@ -76,6 +76,27 @@ def test_validation_rejects_before_launch(pkg):
     assert 0 < L.qmi_grpo_fused_workspace_bytes(32, 512) < 4096
     assert L.qmi_ppo_clipped_loss(None, None, None, None, 1, 0, 2, 3, 0.2, 0, None, None, None) == -1
     assert L.qmi_ppo_clipped_loss(fake, fake, fake, fake, 1, 0, 2, 3, 0.2, 7, fake, None, None) == -4
+    # fused lm_head: zero rows is a no-op; k above 64, hidden not a multiple of
+    # 64, a non-positive temperature, a short workspace and a row count whose
+    # item kernel would overflow its 32-bit item / step counts are rejected
+    ws = L.qmi_lm_head_workspace_bytes(4, 151936, 0)
+    assert ws >= 4 * (151936 // 32) * 8
+
+    def sample(n_rows, hidden=1024, temp=1.0, top_k=0, ws_bytes=ws):
+        return L.qmi_lm_head_sample(fake, 1024, n_rows, fake, 1024, 151936, hidden, temp, top_k,
+                                    0, 0, None, fake, None, fake, ws_bytes, None)
+
+    assert sample(0) == 0
+    assert sample(4, top_k=65) == -4
+    assert sample(4, hidden=1000) == -4
+    assert sample(4, temp=0.0) == -2
+    assert sample(4, ws_bytes=ws - 8) == -5
+    assert sample(8_000_000, ws_bytes=1 << 62) == -4
+    assert sample(7_000_000, ws_bytes=1 << 62, temp=0.0) == -2  # within the item-count limit
+    assert L.qmi_lm_head_logprob(fake, 1024, 8_000_000, fake, 1024, 151936, 1024, fake, 1, fake,
+                                 None, fake, 1 << 62, None) == -4
+    assert L.qmi_lm_head_logprob(fake, 1024, 4, fake, 1024, 151936, 1024, None, 1, fake,
+                                 None, fake, ws, None) == -1
 
 
 def test_product_fails_loudly_without_library(pkg, monkeypatch, tmp_path):
