@@ -375,3 +375,56 @@ def test_forward_logprob_without_grad_is_fused(pkg, gpu):
     lse = torch.logsumexp(xr, -1)
     assert lp.shape == ids.shape
     assert _lp_err(lp.cpu().reshape(-1), xr, lo, hi, ids.cpu().reshape(-1), lse).max() <= LP_TOL
+
+
+# Shapes at the kernels' edges: vocabularies below one 32-entry slice or one
+# 128-entry tile, or one entry past them; hidden sizes of one 64-wide chunk, three
+# chunks and 2,048; the row counts on both sides of each configuration change
+# (64 / 65, 256 / 257); top-1 and top-64.
+EDGE_CASES = [  # (rows, vocab, hidden, top_k, temperature)
+    (1, 7, 64, None, 1.0),
+    (3, 33, 64, None, 0.7),
+    (5, 129, 128, 1, 1.0),
+    (64, 200, 2048, None, 1.0),
+    (65, 200, 2048, 20, 1.0),
+    (256, 1000, 192, None, 1.3),
+    (257, 1000, 192, 64, 1.0),
+    (511, 131, 64, 20, 0.9),
+]
+
+
+@pytest.mark.parametrize("n,vocab,hidden,k,temp", EDGE_CASES)
+def test_lm_head_edge_shapes(pkg, gpu, n, vocab, hidden, k, temp):
+    """Sampling (all entries or top k) and the target log-prob at edge shapes,
+    against the oracle with the bars above."""
+    h, w, hg, wg = _inputs(gpu, n, vocab, hidden=hidden, w_std=0.3 / hidden ** 0.5 * 8,
+                           seed=n + vocab + hidden)
+    seed, offset = 900 + n, 11
+    print(f"[lm_head] edge n={n} vocab={vocab} hidden={hidden} k={k} T={temp}", flush=True)
+    tok, lp = pkg.kernels.lm_head_sample(hg, wg, temp, seed=seed, offset=offset, top_k=k)
+    tgt = torch.randint(0, vocab, (n,), generator=torch.Generator().manual_seed(n))
+    tgt[0] = vocab - 1
+    lpt, lse = pkg.kernels.lm_head_logprob(hg, wg, tgt.to(gpu))
+    torch.cuda.synchronize()
+    tok, lp, lpt, lse = tok.cpu(), lp.cpu(), lpt.cpu(), lse.cpu()
+    xr, lo, hi = _logits_bf16(h, w)
+    u = OS.uniform53(n, seed, offset)
+    assert ((tok >= 0) & (tok < vocab)).all()
+    if k is None or k >= vocab:
+        _assert_draws_close(tok.numpy(), OS.inverse_cdf_draw(xr, temp, u))
+        ref_lse = torch.logsumexp(xr / temp, -1)
+        assert _lp_err(lp, xr / temp, lo / temp, hi / temp, tok, ref_lse).max().item() <= LP_TOL
+    else:
+        amb = (lo != hi).any(-1).numpy()
+        keep = OS.topk_mask(xr, k)
+        inset = keep[np.arange(n), tok.numpy()]
+        assert (inset | amb).all()
+        want = OS.topk_inverse_cdf_draw(xr, k, temp, u)
+        bad = np.flatnonzero((tok.numpy() != want) & ~amb)
+        assert len(bad) <= max(1, n // 100), (bad, tok.numpy()[bad], want[bad])
+        ref = OS.topk_logprobs(xr, k, temp).gather(-1, tok[:, None])[:, 0]
+        err = ((lp.double() - ref).abs() / ref.abs().clamp_min(1.0)).numpy()
+        assert (err[~amb & inset] <= LP_TOL).all(), err.max()
+    ref_lse = torch.logsumexp(xr, -1)
+    assert _lp_err(lpt, xr, lo, hi, tgt, ref_lse).max().item() <= LP_TOL
+    assert _rel(lse, ref_lse) <= LP_TOL
