@@ -16,7 +16,7 @@ pytestmark = pytest.mark.gpu
 
 # (K, N) of the Qwen3-0.6B decode projections, plus a small generic one.
 SHAPES = {"qkv": (1024, 4096), "o_proj": (2048, 1024), "down": (3072, 1024), "small": (256, 48)}
-ROWS = (1, 7, 64, 100, 256)
+ROWS = (1, 7, 64, 65, 100, 129, 200, 256)  # 1, 2, 3 and 4 row tiles of 64, partial ones included
 
 
 def _data(gpu, m, k, n, seed):
