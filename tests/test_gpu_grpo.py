@@ -171,3 +171,33 @@ def test_grpo_config2_full_size(pkg, gpu):
                                         adv[:, None] * w["mask"].cpu(), w["mask"].cpu(), 0.2, "seq")
     assert rel_err(res["adv"], adv) <= RTOL
     assert rel_err(res["loss"], rloss) <= RTOL
+
+
+@pytest.mark.parametrize("reduction", ["token", "seq"])
+def test_loss_with_empty_and_single_token_responses(pkg, gpu, reduction):
+    """A sequence whose response mask is all zero contributes 0 to either
+    reduction (its mask sum gets the reference's + 1e-8, so no 0/0) and gets a
+    zero gradient; a one-token response is an ordinary mean over one token.
+    Fused (log-probs from logits) and plain forms against the oracle."""
+    c = _small_case(9, n_seq=8, n_tok=12, vocab=1001)
+    c["mask"][2] = 0.0                 # empty response
+    c["mask"][5] = 0.0
+    c["mask"][5, 0] = 1.0              # a single response token
+    print(f"[grpo] empty / single-token responses ({reduction})", flush=True)
+    res = pkg.kernels.grpo_fused_forward(c["logits"].to(gpu), c["ids"].to(gpu), c["old"].to(gpu),
+                                         c["mask"].to(gpu), c["rewards"].to(gpu),
+                                         c["pids"].to(gpu), 1e-4, 0.2, reduction)
+    new, _ = OG.logprob_gather(c["logits"], c["ids"])
+    adv = OG.advantage(c["rewards"], c["pids"], 1e-4)
+    adv_tok = adv[:, None] * c["mask"]
+    loss, dlp = pkg.kernels.ppo_clipped_loss_fwd(new.to(gpu), c["old"].to(gpu), adv_tok.to(gpu),
+                                                 c["mask"].to(gpu), 0.2, reduction)
+    torch.cuda.synchronize()
+    ref = OG.fused_loss_step(c["logits"], c["ids"], c["old"], c["mask"], c["rewards"], c["pids"],
+                             1e-4, 0.2, reduction)
+    assert torch.isfinite(res["loss"]).all() and torch.isfinite(loss).all()
+    assert rel_err(res["loss"], ref["loss"]) <= RTOL and rel_err(loss, ref["loss"]) <= RTOL
+    tol = 1e-4 * ref["dlp"].abs().max().item() + 1e-7
+    assert (res["dlp"].cpu() - ref["dlp"]).abs().max().item() <= tol
+    assert (dlp.cpu() - ref["dlp"]).abs().max().item() <= tol
+    assert (res["dlp"].cpu()[2] == 0).all() and (dlp.cpu()[2] == 0).all()
